@@ -1,0 +1,227 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized-matmul path (one GPU).
+
+Headline metric: qmv HBM GB/s at K=4096 x N=12288, 4-bit gs64,
+bf16 (config 2a) -> `value`; qmm TFLOP/s at M=512, N=K=4096 (config 3a) -> the
+`qmm` object.  A "step" is one kernel call over one batch of synthetic input
+already resident in HBM.  `--copies` independent weight copies are rotated
+so the working set (>= 450 MB for qmv) exceeds the 256 MB Infinity Cache;
+steps are captured into a HIP graph and replayed, bracketed by HIP events on
+the launch stream.  The CPU baseline leg times the oracle's multithreaded
+dequantize-and-dot on the host.
+
+    python bench.py [--steps K] [--warmup W] [--only qmv|qmm|all] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "qmv HBM GB/s (%peak) K4096×N12288 4b; qmm TFLOPS (%MFMA peak) M=512"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+
+
+def algo_bytes(m, n, k, gs, bits, tsize=2):
+    """Reference byte formula (qmv_dispatch_bench.rs:37-43) extended to M rows."""
+    return n * k * bits // 8 + 2 * n * (k // gs) * tsize + m * k * tsize + m * n * tsize
+
+
+def make_copies(dev, rng, copies, n, k, gs, bits, dtype):
+    from cider_press_amd.synthetic import from_bits, to_bits
+
+    out = []
+    host0 = None
+    for c in range(copies):
+        w = rng.integers(0, 2**32, size=(n, k * bits // 32), dtype=np.uint64).astype(np.uint32)
+        s = to_bits(rng.uniform(0.002, 0.02, size=(n, k // gs)).astype(np.float32), dtype)
+        b = to_bits(-float(1 << (bits - 1)) * from_bits(s, dtype), dtype)
+        if c == 0:
+            host0 = (w, s, b)
+        out.append((dev.upload(w.reshape(-1), "u32"), dev.upload(s.reshape(-1), dtype),
+                    dev.upload(b.reshape(-1), dtype)))
+    return out, host0
+
+
+def time_graph(dev, steps, warmup, encode_step):
+    """Capture `steps` calls in a graph, replay once untimed per warmup batch,
+    then time one replay between HIP events on the launch stream."""
+    from cider_press_amd.kernels import Event
+
+    cmds = dev.commands()
+    if warmup:
+        cmds.begin_capture()
+        for i in range(warmup):
+            encode_step(cmds, i)
+        gw = cmds.end_capture()
+        gw.launch(cmds)
+        cmds.commit_and_wait()
+    cmds.begin_capture()
+    for i in range(steps):
+        encode_step(cmds, i)
+    g = cmds.end_capture()
+    g.launch(cmds)          # one untimed replay of the timed graph itself
+    cmds.commit_and_wait()
+    e0, e1 = Event(), Event()
+    cmds.commit_and_wait()  # barrier: nothing in flight before the timed region
+    e0.record(cmds)
+    g.launch(cmds)
+    e1.record(cmds)
+    cmds.commit_and_wait()
+    return e0.elapsed_ms(e1) / steps
+
+
+def bench_qmv(dev, lib, args, rng):
+    from cider_press_amd.kernels import qmv as kqmv
+    from cider_press_amd.synthetic import make_x
+
+    n, k, gs, bits, dtype = 12288, 4096, 64, 4, "bf16"
+    copies, host0 = make_copies(dev, rng, args.copies, n, k, gs, bits, dtype)
+    x = make_x(rng, 1, k, dtype)
+    X = dev.upload(x.reshape(-1), dtype)
+    Y = dev.alloc_buffer(n, dtype)
+
+    def step(cmds, i):
+        W, S, B = copies[i % len(copies)]
+        kqmv.affine_qmv(cmds, lib, W, S, B, X, Y, k, gs, bits)
+
+    parity = None
+    if not args.no_parity:
+        from oracle import oracle as O  # checker only
+
+        cmds = dev.commands()
+        step(cmds, 0)
+        cmds.commit_and_wait()
+        ref = O.qmm_ref(x, *host0, 1, n, k, gs, bits, dtype)
+        rep = O.tolerance_report(Y.to_numpy().reshape(1, n), ref, x, k, dtype)
+        parity = {"rel_l2": rep["rel_l2"], "max_abs": rep["max_abs"], "ok": rep["ok"]}
+    ms = time_graph(dev, args.steps, args.warmup, step)
+    nbytes = algo_bytes(1, n, k, gs, bits)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"ms": ms, "gbs": gbs, "bytes": nbytes, "parity": parity, "host0": host0, "x": x,
+            "shape": (n, k, gs, bits)}
+
+
+def bench_qmm(dev, lib, args, rng):
+    from cider_press_amd.kernels import qmm as kqmm
+    from cider_press_amd.synthetic import make_x
+
+    m, n, k, gs, bits, dtype = 512, 4096, 4096, 64, 4, "bf16"
+    copies, host0 = make_copies(dev, rng, args.copies, n, k, gs, bits, dtype)
+    x = make_x(rng, m, k, dtype)
+    X = dev.upload(x.reshape(-1), dtype)
+    Y = dev.alloc_buffer(m * n, dtype)
+
+    def step(cmds, i):
+        W, S, B = copies[i % len(copies)]
+        kqmm.affine_qmm_t(cmds, lib, W, S, B, X, Y, m, n, k, gs, bits)
+
+    parity = None
+    if not args.no_parity:
+        from oracle import oracle as O  # checker only
+
+        cmds = dev.commands()
+        step(cmds, 0)
+        cmds.commit_and_wait()
+        ref = O.qmm_ref(x, *host0, m, n, k, gs, bits, dtype, threads=min(16, os.cpu_count() or 1))
+        rep = O.tolerance_report(Y.to_numpy().reshape(m, n), ref, x, k, dtype)
+        parity = {"rel_l2": rep["rel_l2"], "max_abs": rep["max_abs"], "ok": rep["ok"]}
+    ms = time_graph(dev, args.qmm_steps, args.warmup, step)
+    flops = 2.0 * m * n * k
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"ms": ms, "tflops": tflops, "flops": flops, "bytes": algo_bytes(m, n, k, gs, bits),
+            "parity": parity}
+
+
+def cpu_baseline(q, budget_s):
+    """Oracle dequantize-and-dot (T-rounded weights, fp32 accumulate) on the host."""
+    from oracle import oracle as O
+
+    n, k, gs, bits = q["shape"]
+    w, s, b = q["host0"]
+    threads = min(16, os.cpu_count() or 1)
+    O.cpu_baseline(q["x"], w, s, b, 1, n, k, gs, bits, "bf16", threads=threads)  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    times = []
+    while time.perf_counter() - t0 < budget_s and reps < 10000:
+        t1 = time.perf_counter()
+        O.cpu_baseline(q["x"], w, s, b, 1, n, k, gs, bits, "bf16", threads=threads)
+        times.append(time.perf_counter() - t1)
+        reps += 1
+    med = float(np.median(times))
+    return {"value": round(q["bytes"] / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"qmv config 2a (N=12288, K=4096, 4-bit gs64, bf16), median of {reps} calls "
+                      f"over {budget_s:.0f} s, {threads} threads, oracle C dequantize-and-dot"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--qmm-steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--copies", type=int, default=16)
+    ap.add_argument("--only", choices=["qmv", "qmm", "all"], default="all")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(json.dumps({"error": f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported "
+                                   "(the quantized-matmul path is measured on a single MI355X)"}))
+        sys.exit(2)
+
+    from cider_press_amd.kernels import Device, KernelLibrary
+
+    dev = Device.system_default()
+    lib = KernelLibrary.quantized(dev)
+    info = dev.info()
+    rng = np.random.default_rng(0)
+
+    line = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded uniform nibbles, U(0.002,0.02) "
+            "scales, biases=-8*scale, x~N(0,1))",
+            "config": {"workload": "qmv config 2a: x[1,4096] . W[12288,4096]^T, 4-bit gs64, bf16, "
+                                   f"{args.copies} rotated weight copies", "device": info["name"],
+                       "cu_count": info["cu_count"]}}
+    q = None
+    if args.only in ("qmv", "all"):
+        q = bench_qmv(dev, lib, args, rng)
+        line["value"] = round(q["gbs"], 2)
+        line["ms_per_step"] = q["ms"]
+        line["roofline"] = {"bound": "hbm", "achieved": round(q["gbs"], 2), "peak": HBM_PEAK_GBS,
+                            "unit": "GB/s", "frac": round(q["gbs"] / HBM_PEAK_GBS, 4), "traffic": None}
+        line["parity"] = {"qmv": q["parity"]}
+    if args.only in ("qmm", "all"):
+        r = bench_qmm(dev, lib, args, rng)
+        line["qmm"] = {"workload": "config 3a: X[512,4096] . W[4096,4096]^T, 4-bit gs64, bf16",
+                       "value": round(r["tflops"], 2), "unit": "TFLOP/s", "steps": args.qmm_steps,
+                       "ms_per_step": r["ms"],
+                       "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2),
+                                    "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                    "frac": round(r["tflops"] / BF16_MFMA_PEAK_TFLOPS, 4), "traffic": None}}
+        line.setdefault("parity", {})["qmm"] = r["parity"]
+        if args.only == "qmm":
+            line["metric"] = METRIC
+            line["value"] = round(r["tflops"], 2)
+            line["unit"] = "TFLOP/s"
+            line["ms_per_step"] = r["ms"]
+            line["steps"] = args.qmm_steps
+            line["roofline"] = line["qmm"]["roofline"]
+    if q is not None and not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(q, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

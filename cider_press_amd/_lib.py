@@ -1,0 +1,170 @@
+"""ctypes binding of libcpq.so (the HIP library; C ABI in include/cpq.h).
+
+There is no fallback: if the shared library is missing this module raises,
+so nothing silently runs on the CPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libcpq.so")
+
+# cpq_status
+OK = 0
+NO_DEVICE = 1
+KERNEL_NOT_FOUND = 2
+BUFFER_ALLOCATION = 3
+BUFFER_TOO_LARGE = 4
+INVALID_ARGUMENT = 5
+COMMAND_BUFFER_FAILED = 6
+HIP_API = 7
+
+# cpq_dtype
+DTYPES = {"f32": 0, "f16": 1, "bf16": 2}
+
+
+class Error(Exception):
+    """cider_press_kernels::Error analogue; `kind` names the variant."""
+
+    kind = "Error"
+
+    def __init__(self, message: str):
+        super().__init__(message)
+        self.message = message
+
+
+class NoDevice(Error):
+    kind = "NoDevice"
+
+
+class KernelNotFound(Error):
+    kind = "KernelNotFound"
+
+
+class BufferAllocation(Error):
+    kind = "BufferAllocation"
+
+
+class BufferTooLarge(Error):
+    kind = "BufferTooLarge"
+
+
+class InvalidArgument(Error):
+    kind = "InvalidArgument"
+
+
+class CommandBufferFailed(Error):
+    kind = "CommandBufferFailed"
+
+
+class HipApi(Error):
+    kind = "HipApi"
+
+
+_ERRORS = {
+    NO_DEVICE: NoDevice,
+    KERNEL_NOT_FOUND: KernelNotFound,
+    BUFFER_ALLOCATION: BufferAllocation,
+    BUFFER_TOO_LARGE: BufferTooLarge,
+    INVALID_ARGUMENT: InvalidArgument,
+    COMMAND_BUFFER_FAILED: CommandBufferFailed,
+    HIP_API: HipApi,
+}
+
+_c = ctypes
+_vp = _c.c_void_p
+_sz = _c.c_size_t
+_u32 = _c.c_uint32
+_int = _c.c_int
+_st = _c.c_int  # cpq_status
+_pp = _c.POINTER(_c.c_void_p)
+_psz = _c.POINTER(_c.c_size_t)
+
+# name -> (restype, argtypes); the full ABI of include/cpq.h
+SIGNATURES = {
+    "cpq_last_error_message": (_c.c_char_p, []),
+    "cpq_version": (_c.c_char_p, []),
+    "cpq_device_system_default": (_st, [_pp]),
+    "cpq_device_release": (None, [_vp]),
+    "cpq_device_info": (_st, [_vp, _c.c_char_p, _sz, _c.POINTER(_int), _c.POINTER(_int)]),
+    "cpq_alloc_buffer": (_st, [_vp, _sz, _pp, _psz]),
+    "cpq_upload": (_st, [_vp, _vp, _sz, _pp, _psz]),
+    "cpq_free_buffer": (_st, [_vp, _vp]),
+    "cpq_read_buffer": (_st, [_vp, _vp, _vp, _sz]),
+    "cpq_write_buffer": (_st, [_vp, _vp, _vp, _sz]),
+    "cpq_commands_create": (_st, [_vp, _pp]),
+    "cpq_commands_wrap_stream": (_st, [_vp, _vp, _pp]),
+    "cpq_commands_stream": (_vp, [_vp]),
+    "cpq_commands_commit": (_st, [_vp]),
+    "cpq_commands_wait": (_st, [_vp]),
+    "cpq_commands_commit_and_wait": (_st, [_vp]),
+    "cpq_commands_release": (None, [_vp]),
+    "cpq_commands_begin_capture": (_st, [_vp]),
+    "cpq_commands_end_capture": (_st, [_vp, _pp]),
+    "cpq_graph_launch": (_st, [_vp, _vp]),
+    "cpq_graph_release": (None, [_vp]),
+    "cpq_event_create": (_st, [_pp]),
+    "cpq_event_record": (_st, [_vp, _vp]),
+    "cpq_event_elapsed_ms": (_st, [_vp, _vp, _c.POINTER(_c.c_float)]),
+    "cpq_event_release": (None, [_vp]),
+    "cpq_quantization_validate": (_st, [_u32, _u32]),
+    "cpq_packed_word_count": (_st, [_u32, _u32, _sz, _psz]),
+    "cpq_group_count": (_st, [_u32, _u32, _sz, _psz]),
+    "cpq_kernel_available": (_int, [_int, _u32, _u32]),
+    "cpq_affine_qmv": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _u32, _u32]),
+    "cpq_affine_qmm_t": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz,
+                               _u32, _u32]),
+    "cpq_affine_dequantize": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _u32, _u32]),
+    "cpq_affine_gather_qmm": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _vp, _sz, _vp, _sz,
+                                    _sz, _sz, _sz, _u32, _u32, _int]),
+    "cpq_quantized_matmul": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _vp, _sz, _sz, _sz,
+                                   _u32, _u32]),
+    "cpq_check_qmv_args": (_st, [_int, _sz, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
+    "cpq_check_qmm_args": (_st, [_int, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
+    "cpq_check_dequantize_args": (_st, [_int, _sz, _sz, _sz, _sz, _u32, _u32]),
+    "cpq_check_gather_args": (_st, [_int, _sz, _sz, _sz, _sz, _int, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
+    "cpq_qweight_from_bytes": (_st, [_vp, _int, _sz, _sz, _sz, _u32, _u32, _vp, _sz, _vp, _sz, _vp, _sz, _pp]),
+    "cpq_qweight_release": (None, [_vp]),
+    "cpq_tensor_from_host": (_st, [_vp, _int, _psz, _sz, _vp, _pp]),
+    "cpq_tensor_quantized_matmul": (_st, [_vp, _vp, _int, _pp]),
+    "cpq_tensor_dequantize": (_st, [_vp, _pp]),
+    "cpq_tensor_eval": (_st, [_vp]),
+    "cpq_tensor_shape": (_st, [_vp, _psz, _sz, _psz]),
+    "cpq_tensor_read": (_st, [_vp, _vp, _sz]),
+    "cpq_tensor_release": (None, [_vp]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libcpq.so (built by ``python -m cider_press_amd._build``)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m cider_press_amd._build` "
+                "(the HIP library is required; there is no CPU fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    msg = lib().cpq_last_error_message()
+    return msg.decode() if msg else ""
+
+
+def check(status: int) -> None:
+    if status != OK:
+        raise _ERRORS.get(status, Error)(last_error())
+
+
+def status_name(status: int) -> str:
+    return {OK: "Ok"} .get(status) or _ERRORS.get(status, Error).kind

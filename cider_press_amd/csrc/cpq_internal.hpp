@@ -1,0 +1,87 @@
+// Internal declarations shared by the host runtime, the op dispatchers and
+// the HIP kernel launchers of libcpq.so.  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/cpq.h"
+
+struct cpq_device {
+  int ordinal = 0;
+  int cu_count = 0;
+  int clock_khz = 0;
+  int xcd_count = 8;
+  char name[256] = {0};
+  // Session used by Tensor::eval (created on first use, released with the device).
+  struct cpq_commands* eval_session = nullptr;
+};
+
+struct cpq_commands {
+  cpq_device* dev = nullptr;
+  hipStream_t stream = nullptr;
+  bool owns_stream = false;
+  // Device-side status word: kernels that can detect bad data (gather indices)
+  // add to it; cpq_commands_wait reads and clears it.
+  unsigned int* status = nullptr;
+};
+
+struct cpq_event {
+  hipEvent_t ev = nullptr;
+};
+
+struct cpq_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+namespace cpq {
+
+// Per-thread error text (cpq_last_error_message).
+cpq_status fail(cpq_status st, const std::string& msg);
+cpq_status hip_fail(hipError_t e, const char* what);
+
+inline size_t dtype_size(cpq_dtype t) { return t == CPQ_DTYPE_F32 ? 4 : 2; }
+
+bool kernel_available(cpq_dtype dtype, uint32_t group_size, uint32_t bits);
+
+// ---------------------------------------------------------------------------
+// Kernel launchers (defined in kernels/*.hip).  Shapes are validated by the
+// callers; launchers only assert the invariants their grids rely on.
+// ---------------------------------------------------------------------------
+
+struct QuantArgs {
+  const uint32_t* w;   // [rows, K*bits/32] (per expert for gather)
+  const void* scales;  // [rows, K/gs]
+  const void* biases;  // [rows, K/gs]
+  int gs;
+  int bits;
+  cpq_dtype dtype;
+};
+
+hipError_t launch_dequantize(hipStream_t s, const QuantArgs& q, void* out, size_t n_out);
+
+// Decode GEMV: y[N] = x[K] . W^T for one activation row.
+hipError_t launch_qmv(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k);
+
+// Small-M GEMM on the matrix cores with VALU dequantization (M rows, any M;
+// processed 16 rows at a time).  Also the gather kernel body.
+hipError_t launch_qmm_skinny(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m,
+                             int n, int k);
+
+// Prefill GEMM: LDS-tiled bf16/f16 MFMA with the W tile dequantized into LDS.
+hipError_t launch_qmm(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n,
+                      int k);
+
+// Routed experts.
+hipError_t launch_gather_qmm(hipStream_t s, const QuantArgs& q, const void* x, int x_rows,
+                             const uint32_t* lhs, const uint32_t* rhs, int n_rows, void* y,
+                             int n_experts, int n, int k, bool sorted, unsigned int* status);
+
+// Row-count threshold below which cpq_quantized_matmul uses the skinny kernel.
+int skinny_max_m(const QuantArgs& q, int n, int k);
+
+}  // namespace cpq

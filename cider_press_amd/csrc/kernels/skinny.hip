@@ -1,0 +1,355 @@
+// Small-M quantized GEMM and routed-expert gather for gfx950.
+//
+//   skinny:  Y[M,N] = X[M,K] . dequant(W[N,K])^T for M up to a few dozen rows.
+//   gather:  Y[r,:] = X[lhs[r],:] . dequant(W[rhs[r]])^T   (routed experts).
+//
+// Reference semantics: qmm_t_impl (kernels-mlx/.../quantized.h:1087-1213) for
+// the dense case and affine_gather_qmm_rhs / affine_gather_qmm_t
+// (quantized.h:2092-2172, 2242-2436) for the gather case: dequantize W to T,
+// accumulate in fp32, store T.
+//
+// Both are HBM-bound (the weight stream dominates), so a weight is read and
+// dequantized exactly once per workgroup and then multiplied against every
+// activation row on the matrix cores:
+//   - workgroup = 4 waves, one 16-column slab of W (16 output columns);
+//   - each wave walks a quarter of K in 128-element steps; lane l loads the
+//     32-element chunk (bits words, 16 B at 4-bit) of row n0 + l%16 at chunk
+//     4u + l/16, dequantizes it in registers into four 8-element MFMA
+//     B-operand slices, and issues v_mfma_f32_16x16x32_{bf16,f16} against
+//     up to MB 16-row blocks of activations (A operand read straight from
+//     global/L2: activations are tiny next to W);
+//   - the four K-partial 16x16 tiles are summed through LDS.
+// MFMA 16x16x32 operand layout: A[m][k] in lane m + 16*(k/8), element k%8;
+// B[k][n] in lane n + 16*(k/8), element k%8; D[m][n] in lane n + 16*(m/4),
+// element m%4.  Any bijection of k onto (lane group, element) is valid as long
+// as A and B agree; lane group g / slice i / element j <-> k = 32*(4u+g)+8i+j.
+#include "../cpq_internal.hpp"
+#include "common.hpp"
+
+namespace cpq {
+namespace {
+
+using namespace dev;
+
+template <typename TT>
+struct Mfma16;
+template <>
+struct Mfma16<BF16> {
+  static __device__ __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma16<F16> {
+  static __device__ __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+constexpr int kWaves = 4;
+constexpr int kMaxMB = 4;  // up to 64 activation rows per pass
+
+struct TileShared {
+  const uint16_t* xrow[16 * kMaxMB];  // activation row per local row (nullptr: zero row)
+  uint16_t* yrow[16 * kMaxMB];        // output row per local row (nullptr: not stored)
+  float red[kWaves][kMaxMB][64][4];   // K-partial tiles
+  int rows[16 * kMaxMB];              // gather: global row ids of this pass
+  int count;
+  int pos;
+};
+
+// One 16-column slab of W against up to 16*MB activation rows (pointers in sh).
+// All 256 threads must call it (contains __syncthreads).
+template <typename TT, int BITS, int MB>
+__device__ __forceinline__ void skinny_tile(const uint32_t* __restrict__ w,
+                                            const uint16_t* __restrict__ scales,
+                                            const uint16_t* __restrict__ biases, int n, int k,
+                                            int gs_shift, int n0, TileShared& sh) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nl = lane & 15;
+  const int g = lane >> 4;
+  const int col = n0 + nl;
+  const bool col_ok = col < n;
+  const int chunks = k >> 5;
+  const int units = (chunks + 3) >> 2;
+  const size_t words_per_row = (size_t)k * BITS / 32;
+  const int groups_per_row = k >> gs_shift;
+  const uint32_t* wrow = w + (size_t)(col_ok ? col : 0) * words_per_row;
+  const uint16_t* srow = scales + (size_t)(col_ok ? col : 0) * groups_per_row;
+  const uint16_t* brow = biases + (size_t)(col_ok ? col : 0) * groups_per_row;
+
+  const uint16_t* xr[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) xr[mb] = sh.xrow[16 * mb + nl];
+
+  f32x4 acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int u = wave; u < units; u += kWaves) {
+    const int c = 4 * u + g;
+    const bool live = c < chunks;
+    uint32_t wp[16];
+    if (live && col_ok) {
+      uint32_t wv[BITS];
+      load_chunk<BITS>(wrow, (size_t)c, wv);
+      const int gi = (c << 5) >> gs_shift;
+      dequant_chunk<TT, BITS>(wv, TT::to_f32(srow[gi]), TT::to_f32(brow[gi]), wp);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) wp[i] = 0u;
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      u32x4 a[4];
+      if (live && xr[mb]) {
+        const u32x4* xs = reinterpret_cast<const u32x4*>(xr[mb] + (size_t)c * 32);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = xs[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        u32x4 b = {wp[4 * i], wp[4 * i + 1], wp[4 * i + 2], wp[4 * i + 3]};
+        acc[mb] = Mfma16<TT>::run(a[i], b, acc[mb]);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sh.red[wave][mb][lane][i] = acc[mb][i];
+  }
+  __syncthreads();
+  // Each wave finishes MB/4 (at least one) of the 16-row blocks.
+  for (int mb = wave; mb < MB; mb += kWaves) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = sh.red[0][mb][lane][i] + sh.red[1][mb][lane][i] + sh.red[2][mb][lane][i] +
+                sh.red[3][mb][lane][i];
+      const int m = 16 * mb + 4 * g + i;  // D row of element i in this lane
+      uint16_t* yr = sh.yrow[m];
+      if (yr && col_ok) yr[col] = TT::from_f32(v);
+    }
+  }
+  __syncthreads();
+}
+
+template <typename TT, int BITS, int MB>
+__global__ __launch_bounds__(256) void skinny_kernel(const uint32_t* __restrict__ w,
+                                                     const uint16_t* __restrict__ scales,
+                                                     const uint16_t* __restrict__ biases,
+                                                     const uint16_t* __restrict__ x,
+                                                     uint16_t* __restrict__ y, int m, int n, int k,
+                                                     int gs_shift) {
+  __shared__ TileShared sh;
+  const int n0 = blockIdx.x * 16;
+  const int row0 = blockIdx.y * 16 * MB;
+  if (threadIdx.x < 16 * MB) {
+    const int r = row0 + threadIdx.x;
+    sh.xrow[threadIdx.x] = r < m ? x + (size_t)r * k : nullptr;
+    sh.yrow[threadIdx.x] = r < m ? y + (size_t)r * n : nullptr;
+  }
+  __syncthreads();
+  skinny_tile<TT, BITS, MB>(w, scales, biases, n, k, gs_shift, n0, sh);
+}
+
+// Routed experts: workgroup (16-column slab, expert e).  Rows routed to e are
+// gathered 64 at a time (ballot compaction over rhs, or a binary-searched run
+// when rhs is sorted), then run through skinny_tile against W[e].  Rows whose
+// lhs index is out of range are skipped here and zeroed by gather_check_kernel.
+template <typename TT, int BITS>
+__global__ __launch_bounds__(256) void gather_kernel(
+    const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
+    const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, int x_rows,
+    const uint32_t* __restrict__ lhs, const uint32_t* __restrict__ rhs, int n_rows,
+    uint16_t* __restrict__ y, int n, int k, int gs_shift, int sorted) {
+  __shared__ TileShared sh;
+  const int n0 = blockIdx.x * 16;
+  const uint32_t e = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const size_t expert_words = (size_t)n * k * BITS / 32;
+  const size_t expert_groups = (size_t)n * (k >> gs_shift);
+  const uint32_t* we = w + e * expert_words;
+  const uint16_t* se = scales + e * expert_groups;
+  const uint16_t* be = biases + e * expert_groups;
+
+  int lo = 0, hi = n_rows;
+  if (sorted) {
+    // [lo, hi) = equal range of e in the ascending rhs (gather_qmm_rhs walks
+    // these runs, quantized.h:2329-2345).
+    int a = 0, b = n_rows;
+    while (a < b) { int mid = (a + b) >> 1; if (rhs[mid] < e) a = mid + 1; else b = mid; }
+    lo = a;
+    b = n_rows;
+    while (a < b) { int mid = (a + b) >> 1; if (rhs[mid] <= e) a = mid + 1; else b = mid; }
+    hi = a;
+  }
+  if (threadIdx.x == 0) sh.pos = lo;
+  __syncthreads();
+
+  while (true) {
+    const int pos = sh.pos;
+    if (pos >= hi) break;
+    if (wave == 0) {
+      int p = pos, cnt = 0;
+      if (sorted) {
+        cnt = min(64, hi - p);
+        if (lane < cnt) sh.rows[lane] = p + lane;
+        p += cnt;
+      } else {
+        while (p < hi && cnt < 64) {
+          const int r = p + lane;
+          const bool match = r < hi && rhs[r] == e;
+          const unsigned long long mask = __ballot(match);
+          const int rank = __popcll(mask & ((1ull << lane) - 1ull));
+          const bool take = match && (cnt + rank < 64);
+          if (take) sh.rows[cnt + rank] = r;
+          const unsigned long long left = mask & ~__ballot(take);
+          const int took = __popcll(mask) - __popcll(left);
+          cnt += took;
+          p = left ? p + (int)__ffsll((long long)left) - 1 : p + 64;
+        }
+      }
+      if (lane == 0) {
+        sh.count = cnt;
+        sh.pos = p;
+      }
+    }
+    __syncthreads();
+    const int cnt = sh.count;
+    if (threadIdx.x < 64) {
+      const int i = threadIdx.x;
+      const uint16_t* xp = nullptr;
+      uint16_t* yp = nullptr;
+      if (i < cnt) {
+        const int r = sh.rows[i];
+        const uint32_t xi = lhs ? lhs[r] : (uint32_t)r;
+        if (xi < (uint32_t)x_rows) {
+          xp = x + (size_t)xi * k;
+          yp = y + (size_t)r * n;
+        }
+      }
+      sh.xrow[i] = xp;
+      sh.yrow[i] = yp;
+    }
+    __syncthreads();
+    if (cnt <= 16) {
+      skinny_tile<TT, BITS, 1>(we, se, be, n, k, gs_shift, n0, sh);
+    } else if (cnt <= 32) {
+      skinny_tile<TT, BITS, 2>(we, se, be, n, k, gs_shift, n0, sh);
+    } else {
+      skinny_tile<TT, BITS, 4>(we, se, be, n, k, gs_shift, n0, sh);
+    }
+  }
+}
+
+// Validates routing indices on the device: out-of-range rows are zeroed and
+// counted; with sorted=1 every descent is counted too.
+template <typename TT>
+__global__ __launch_bounds__(256) void gather_check_kernel(const uint32_t* __restrict__ lhs,
+                                                           const uint32_t* __restrict__ rhs,
+                                                           int n_rows, int x_rows, int n_experts,
+                                                           int sorted, uint16_t* __restrict__ y,
+                                                           int n, unsigned int* status) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= n_rows) return;
+  const bool bad = rhs[r] >= (uint32_t)n_experts || (lhs && lhs[r] >= (uint32_t)x_rows);
+  const bool unsorted = sorted && r + 1 < n_rows && rhs[r] > rhs[r + 1];
+  if (bad) {
+    for (int j = 0; j < n; ++j) y[(size_t)r * n + j] = 0;
+  }
+  if (bad || unsorted) atomicAdd(status, 1u);
+}
+
+int shift_of(int gs) {
+  int s = 0;
+  while ((1 << s) < gs) ++s;
+  return s;
+}
+
+template <typename TT, int BITS>
+hipError_t launch_skinny_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n,
+                           int k) {
+  const int gs_shift = shift_of(q.gs);
+  const int mb = (m + 15) / 16;
+  const auto* sc = static_cast<const uint16_t*>(q.scales);
+  const auto* bi = static_cast<const uint16_t*>(q.biases);
+  const auto* xx = static_cast<const uint16_t*>(x);
+  auto* yy = static_cast<uint16_t*>(y);
+  const unsigned gx = (unsigned)((n + 15) / 16);
+  if (mb <= 1) {
+    hipLaunchKernelGGL((skinny_kernel<TT, BITS, 1>), dim3(gx, 1), dim3(256), 0, s, q.w, sc, bi, xx,
+                       yy, m, n, k, gs_shift);
+  } else if (mb <= 2) {
+    hipLaunchKernelGGL((skinny_kernel<TT, BITS, 2>), dim3(gx, 1), dim3(256), 0, s, q.w, sc, bi, xx,
+                       yy, m, n, k, gs_shift);
+  } else {
+    const unsigned gy = (unsigned)((m + 63) / 64);
+    hipLaunchKernelGGL((skinny_kernel<TT, BITS, 4>), dim3(gx, gy), dim3(256), 0, s, q.w, sc, bi,
+                       xx, yy, m, n, k, gs_shift);
+  }
+  return hipGetLastError();
+}
+
+template <typename TT, int BITS>
+hipError_t launch_gather_t(hipStream_t s, const QuantArgs& q, const void* x, int x_rows,
+                           const uint32_t* lhs, const uint32_t* rhs, int n_rows, void* y,
+                           int n_experts, int n, int k, bool sorted, unsigned int* status) {
+  if (n_rows == 0) return hipSuccess;
+  const int gs_shift = shift_of(q.gs);
+  hipLaunchKernelGGL((gather_check_kernel<TT>), dim3((n_rows + 255) / 256), dim3(256), 0, s, lhs,
+                     rhs, n_rows, x_rows, n_experts, (int)sorted, static_cast<uint16_t*>(y), n,
+                     status);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((gather_kernel<TT, BITS>), dim3((unsigned)((n + 15) / 16), (unsigned)n_experts),
+                     dim3(256), 0, s, q.w, static_cast<const uint16_t*>(q.scales),
+                     static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x),
+                     x_rows, lhs, rhs, n_rows, static_cast<uint16_t*>(y), n, k, gs_shift,
+                     (int)sorted);
+  return hipGetLastError();
+}
+
+#define CPQ_BITS_SWITCH(FN, TT, ...)                 \
+  switch (q.bits) {                                  \
+    case 2: return FN<TT, 2>(__VA_ARGS__);           \
+    case 3: return FN<TT, 3>(__VA_ARGS__);           \
+    case 4: return FN<TT, 4>(__VA_ARGS__);           \
+    case 5: return FN<TT, 5>(__VA_ARGS__);           \
+    case 6: return FN<TT, 6>(__VA_ARGS__);           \
+    case 8: return FN<TT, 8>(__VA_ARGS__);           \
+    default: return hipErrorInvalidValue;            \
+  }
+
+}  // namespace
+
+hipError_t launch_qmm_skinny(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m,
+                             int n, int k) {
+  if (q.dtype == CPQ_DTYPE_BF16) { CPQ_BITS_SWITCH(launch_skinny_t, BF16, s, q, x, y, m, n, k) }
+  if (q.dtype == CPQ_DTYPE_F16) { CPQ_BITS_SWITCH(launch_skinny_t, F16, s, q, x, y, m, n, k) }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_gather_qmm(hipStream_t s, const QuantArgs& q, const void* x, int x_rows,
+                             const uint32_t* lhs, const uint32_t* rhs, int n_rows, void* y,
+                             int n_experts, int n, int k, bool sorted, unsigned int* status) {
+  if (q.dtype == CPQ_DTYPE_BF16) {
+    CPQ_BITS_SWITCH(launch_gather_t, BF16, s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k,
+                    sorted, status)
+  }
+  if (q.dtype == CPQ_DTYPE_F16) {
+    CPQ_BITS_SWITCH(launch_gather_t, F16, s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k,
+                    sorted, status)
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace cpq

@@ -1,0 +1,386 @@
+// Op entry points of libcpq.so: argument validation, kernel selection, launch.
+//
+// Host-side mirror of the reference's typed dispatch functions:
+//   crates/cider-press-kernels/src/kernels/qmv.rs:77-205         -> cpq_affine_qmv
+//   crates/cider-press-kernels/src/kernels/qmm.rs:66-220         -> cpq_affine_qmm_t
+//   crates/cider-press-kernels/src/kernels/dequantize.rs:58-137  -> cpq_affine_dequantize
+//   crates/cider-press-runtime/src/eval.rs:1293-1394             -> cpq_quantized_matmul
+// Validation order and messages follow those functions so error behaviour is
+// the same; "kernel not found" is reported after shape validation, as the
+// reference's pipeline lookup is (qmv.rs:172-173, library.rs:264-286).
+#include <climits>
+#include <string>
+
+#include "cpq_internal.hpp"
+
+namespace cpq {
+
+bool kernel_available(cpq_dtype dtype, uint32_t group_size, uint32_t bits) {
+  const bool t_ok = dtype == CPQ_DTYPE_BF16 || dtype == CPQ_DTYPE_F16;
+  const bool gs_ok = group_size == 32 || group_size == 64 || group_size == 128;
+  const bool b_ok = bits == 2 || bits == 3 || bits == 4 || bits == 5 || bits == 6 || bits == 8;
+  return t_ok && gs_ok && b_ok;
+}
+
+int skinny_max_m(const QuantArgs& q, int n, int k) {
+  (void)q;
+  (void)n;
+  (void)k;
+  return 32;
+}
+
+namespace {
+
+const char* tname(cpq_dtype t) {
+  return t == CPQ_DTYPE_BF16 ? "bfloat16_t" : t == CPQ_DTYPE_F16 ? "float16_t" : "float";
+}
+
+std::string kname(const char* op, cpq_dtype t, uint32_t gs, uint32_t bits) {
+  return std::string("affine_") + op + "_" + tname(t) + "_gs_" + std::to_string(gs) + "_b_" +
+         std::to_string(bits);
+}
+
+cpq_status not_found(const char* op, cpq_dtype t, uint32_t gs, uint32_t bits) {
+  return fail(CPQ_ERR_KERNEL_NOT_FOUND, "kernel `" + kname(op, t, gs, bits) + "` not found in library");
+}
+
+cpq_status launched(hipError_t e, const char* what) {
+  if (e != hipSuccess) return hip_fail(e, what);
+  return CPQ_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned2(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1u) == 0; }
+
+cpq_status check_ptrs(const char* op, const void* w, const void* s, const void* b, const void* x,
+                      const void* y) {
+  if (!w || !s || !b || !x || !y)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, std::string(op) + ": NULL buffer");
+  if (!aligned16(w) || !aligned16(x) || !aligned16(y) || !aligned2(s) || !aligned2(b))
+    return fail(CPQ_ERR_INVALID_ARGUMENT,
+                std::string(op) + ": w_q, x and y must be 16-byte aligned; scales/biases 2-byte");
+  return CPQ_OK;
+}
+
+cpq_status check_dtype(const char* op, cpq_dtype t) {
+  if (t != CPQ_DTYPE_F32 && t != CPQ_DTYPE_F16 && t != CPQ_DTYPE_BF16)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, std::string(op) + ": unknown dtype " + std::to_string(int(t)));
+  return CPQ_OK;
+}
+
+// Checked a*b (size_t); false on overflow.
+bool mul_ok(size_t a, size_t b, size_t* out) {
+  if (a != 0 && b > SIZE_MAX / a) return false;
+  *out = a * b;
+  return true;
+}
+
+}  // namespace
+}  // namespace cpq
+
+using cpq::fail;
+
+extern "C" {
+
+// ---------------------------------------------------------------------------
+// Validators
+// ---------------------------------------------------------------------------
+
+// qmv.rs:89-163
+cpq_status cpq_check_qmv_args(cpq_dtype dtype, size_t w_q_len, size_t scales_len,
+                              size_t biases_len, size_t x_alloc_bytes, size_t y_len,
+                              size_t in_vec_size, uint32_t group_size, uint32_t bits) {
+  cpq_status st = cpq::check_dtype("affine_qmv", dtype);
+  if (st != CPQ_OK) return st;
+  if (in_vec_size > (size_t)INT_MAX)
+    return fail(CPQ_ERR_INVALID_ARGUMENT,
+                "affine_qmv: K=" + std::to_string(in_vec_size) + " does not fit in i32");
+  const size_t required = in_vec_size * cpq::dtype_size(dtype);
+  if (x_alloc_bytes < required)
+    return fail(CPQ_ERR_INVALID_ARGUMENT,
+                "affine_qmv: activation allocation too small for K-padded read: alloc_len=" +
+                    std::to_string(x_alloc_bytes) + " < required_bytes=" + std::to_string(required) +
+                    " (K-padding requires capacity >= physical K * sizeof(T))");
+  if (y_len > (size_t)INT_MAX)
+    return fail(CPQ_ERR_INVALID_ARGUMENT,
+                "affine_qmv: N=" + std::to_string(y_len) + " does not fit in i32");
+  const long k = (long)in_vec_size, n = (long)y_len;
+  if (k <= 0 || n <= 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmv: K (" + std::to_string(k) + ") and N (" +
+                                              std::to_string(n) + ") must be positive");
+  if (group_size == 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmv: group_size must be positive");
+  if ((size_t)k % group_size != 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmv: K (" + std::to_string(k) +
+                                              ") must be a multiple of group_size (" +
+                                              std::to_string(group_size) + ")");
+  const size_t groups_per_row = (size_t)k / group_size;
+  const size_t expected_w_q = (size_t)n * (size_t)k * bits / 32;
+  if (w_q_len != expected_w_q)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmv: w_q.len()=" + std::to_string(w_q_len) +
+                                              " != N*K*bits/32 (" + std::to_string(expected_w_q) + ")");
+  const size_t expected_groups = (size_t)n * groups_per_row;
+  if (scales_len != expected_groups)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmv: scales.len()=" + std::to_string(scales_len) +
+                                              " != N*K/group_size (" +
+                                              std::to_string(expected_groups) + ")");
+  if (biases_len != expected_groups)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmv: biases.len()=" + std::to_string(biases_len) +
+                                              " != N*K/group_size (" +
+                                              std::to_string(expected_groups) + ")");
+  if (!cpq::kernel_available(dtype, group_size, bits))
+    return cpq::not_found((((size_t)n % 8 == 0) && ((size_t)k % 512 == 0)) ? "qmv_fast" : "qmv",
+                          dtype, group_size, bits);
+  return CPQ_OK;
+}
+
+// qmm.rs:80-119 and validate_qmm_buffer_lens (qmm.rs:165-220)
+cpq_status cpq_check_qmm_args(cpq_dtype dtype, size_t w_q_len, size_t scales_len,
+                              size_t biases_len, size_t x_len, size_t y_len, size_t m, size_t n,
+                              size_t k, uint32_t group_size, uint32_t bits) {
+  cpq_status st = cpq::check_dtype("affine_qmm_t", dtype);
+  if (st != CPQ_OK) return st;
+  if (m > (size_t)INT_MAX)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: M=" + std::to_string(m) + " does not fit in i32");
+  if (n > (size_t)INT_MAX)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: N=" + std::to_string(n) + " does not fit in i32");
+  if (k > (size_t)INT_MAX)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: K=" + std::to_string(k) + " does not fit in i32");
+  if (m == 0 || n == 0 || k == 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: M (" + std::to_string(m) + "), N (" +
+                                              std::to_string(n) + "), K (" + std::to_string(k) +
+                                              ") must all be positive");
+  if (group_size == 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: group_size must be positive");
+  if (k % group_size != 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: K (" + std::to_string(k) +
+                                              ") must be a multiple of group_size (" +
+                                              std::to_string(group_size) + ")");
+  if (n % 32 != 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: N (" + std::to_string(n) +
+                                              ") must be a multiple of 32 (aligned variant only)");
+  size_t nk, nkb, groups, mk, mn;
+  if (!cpq::mul_ok(n, k, &nk))
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: N*K overflows usize");
+  if (!cpq::mul_ok(nk, bits, &nkb))
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: N*K*bits overflows usize");
+  const size_t expected_w_q = nkb / 32;
+  if (w_q_len != expected_w_q)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: w_q.len()=" + std::to_string(w_q_len) +
+                                              " != N*K*bits/32 (" + std::to_string(expected_w_q) + ")");
+  if (!cpq::mul_ok(n, k / group_size, &groups))
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: N*(K/group_size) overflows usize");
+  if (scales_len != groups)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: scales.len()=" + std::to_string(scales_len) +
+                                              " != N*K/group_size (" + std::to_string(groups) + ")");
+  if (biases_len != groups)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: biases.len()=" + std::to_string(biases_len) +
+                                              " != N*K/group_size (" + std::to_string(groups) + ")");
+  if (!cpq::mul_ok(m, k, &mk)) return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: M*K overflows usize");
+  if (x_len != mk)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: x.len()=" + std::to_string(x_len) +
+                                              " != M*K (" + std::to_string(mk) + ")");
+  if (!cpq::mul_ok(m, n, &mn)) return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: M*N overflows usize");
+  if (y_len != mn)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: y.len()=" + std::to_string(y_len) +
+                                              " != M*N (" + std::to_string(mn) + ")");
+  if (!cpq::kernel_available(dtype, group_size, bits))
+    return cpq::not_found("qmm_t", dtype, group_size, bits);
+  return CPQ_OK;
+}
+
+// dequantize.rs:66-104, generalised over (T, group_size, bits)
+cpq_status cpq_check_dequantize_args(cpq_dtype dtype, size_t w_q_len, size_t scales_len,
+                                     size_t biases_len, size_t out_len, uint32_t group_size,
+                                     uint32_t bits) {
+  cpq_status st = cpq::check_dtype("affine_dequantize", dtype);
+  if (st != CPQ_OK) return st;
+  if (out_len == 0) return CPQ_OK;
+  if (bits == 0 || bits > 8)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_dequantize: bits " + std::to_string(bits) +
+                                              " outside 1..=8");
+  // Elements per packed unit (per byte for 2/4/8-bit, per 3- or 5-byte pack otherwise).
+  const size_t pack_factor = (bits == 3 || bits == 5) ? 8 : (bits == 6 ? 4 : 8 / bits);
+  if (out_len % pack_factor != 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_dequantize: out element count " +
+                                              std::to_string(out_len) +
+                                              " not a multiple of pack_factor " +
+                                              std::to_string(pack_factor));
+  if (group_size == 0 || out_len % group_size != 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_dequantize: out element count " +
+                                              std::to_string(out_len) +
+                                              " not a multiple of group_size " +
+                                              std::to_string(group_size));
+  const size_t groups = out_len / group_size;
+  if (scales_len != groups || biases_len != groups)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_dequantize: scales/biases length mismatch (expected " +
+                                              std::to_string(groups) + ", got scales=" +
+                                              std::to_string(scales_len) + ", biases=" +
+                                              std::to_string(biases_len) + ")");
+  size_t total_bits;
+  if (!cpq::mul_ok(out_len, bits, &total_bits))
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_dequantize: out_len*bits overflows usize");
+  const size_t expected = total_bits / 32;
+  if (total_bits % 32 != 0 || w_q_len != expected)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_dequantize: w_q length " + std::to_string(w_q_len) +
+                                              " != expected uint32 count " + std::to_string(expected));
+  if (!cpq::kernel_available(dtype, group_size, bits))
+    return cpq::not_found("dequantize", dtype, group_size, bits);
+  return CPQ_OK;
+}
+
+cpq_status cpq_check_gather_args(cpq_dtype dtype, size_t x_rows, size_t w_q_len,
+                                 size_t scales_len, size_t biases_len, int has_lhs,
+                                 size_t n_rows, size_t y_len, size_t n_experts, size_t n,
+                                 size_t k, uint32_t group_size, uint32_t bits) {
+  cpq_status st = cpq::check_dtype("affine_gather_qmm", dtype);
+  if (st != CPQ_OK) return st;
+  if (n_rows > (size_t)INT_MAX || x_rows > (size_t)INT_MAX || n > (size_t)INT_MAX ||
+      k > (size_t)INT_MAX || n_experts > 65535)
+    return fail(CPQ_ERR_INVALID_ARGUMENT,
+                "affine_gather_qmm: n_rows, x_rows, N, K must fit in i32 and n_experts <= 65535");
+  if (n == 0 || k == 0 || n_experts == 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_gather_qmm: N (" + std::to_string(n) + "), K (" +
+                                              std::to_string(k) + ") and n_experts (" +
+                                              std::to_string(n_experts) + ") must be positive");
+  if (group_size == 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_gather_qmm: group_size must be positive");
+  if (k % group_size != 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_gather_qmm: K (" + std::to_string(k) +
+                                              ") must be a multiple of group_size (" +
+                                              std::to_string(group_size) + ")");
+  if (!has_lhs && x_rows != n_rows)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_gather_qmm: without lhs_indices x must have n_rows (" +
+                                              std::to_string(n_rows) + ") rows, got " +
+                                              std::to_string(x_rows));
+  size_t per_w, w_total, per_g, g_total, yn;
+  if (!cpq::mul_ok(n, k, &per_w) || !cpq::mul_ok(per_w, bits, &per_w) ||
+      !cpq::mul_ok(per_w / 32, n_experts, &w_total))
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_gather_qmm: n_experts*N*K*bits overflows usize");
+  if (w_q_len != w_total)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_gather_qmm: w_q.len()=" + std::to_string(w_q_len) +
+                                              " != n_experts*N*K*bits/32 (" + std::to_string(w_total) + ")");
+  if (!cpq::mul_ok(n, k / group_size, &per_g) || !cpq::mul_ok(per_g, n_experts, &g_total))
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_gather_qmm: group count overflows usize");
+  if (scales_len != g_total || biases_len != g_total)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_gather_qmm: scales/biases length mismatch (expected " +
+                                              std::to_string(g_total) + ", got scales=" +
+                                              std::to_string(scales_len) + ", biases=" +
+                                              std::to_string(biases_len) + ")");
+  if (!cpq::mul_ok(n_rows, n, &yn) || y_len != yn)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_gather_qmm: y.len()=" + std::to_string(y_len) +
+                                              " != n_rows*N (" + std::to_string(n_rows * n) + ")");
+  if (!cpq::kernel_available(dtype, group_size, bits))
+    return cpq::not_found("gather_qmm", dtype, group_size, bits);
+  return CPQ_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Ops
+// ---------------------------------------------------------------------------
+
+cpq_status cpq_affine_qmv(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q,
+                          size_t w_q_len, const void* scales, size_t scales_len,
+                          const void* biases, size_t biases_len, const void* x,
+                          size_t x_alloc_bytes, void* y, size_t y_len, size_t in_vec_size,
+                          uint32_t group_size, uint32_t bits) {
+  if (!cmds) return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmv: NULL command session");
+  cpq_status st = cpq_check_qmv_args(dtype, w_q_len, scales_len, biases_len, x_alloc_bytes, y_len,
+                                     in_vec_size, group_size, bits);
+  if (st != CPQ_OK) return st;
+  st = cpq::check_ptrs("affine_qmv", w_q, scales, biases, x, y);
+  if (st != CPQ_OK) return st;
+  cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
+  return cpq::launched(cpq::launch_qmv(cmds->stream, q, x, y, (int)y_len, (int)in_vec_size),
+                       "affine_qmv launch");
+}
+
+cpq_status cpq_affine_qmm_t(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q,
+                            size_t w_q_len, const void* scales, size_t scales_len,
+                            const void* biases, size_t biases_len, const void* x, size_t x_len,
+                            void* y, size_t y_len, size_t m, size_t n, size_t k,
+                            uint32_t group_size, uint32_t bits) {
+  if (!cmds) return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t: NULL command session");
+  cpq_status st = cpq_check_qmm_args(dtype, w_q_len, scales_len, biases_len, x_len, y_len, m, n, k,
+                                     group_size, bits);
+  if (st != CPQ_OK) return st;
+  st = cpq::check_ptrs("affine_qmm_t", w_q, scales, biases, x, y);
+  if (st != CPQ_OK) return st;
+  cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
+  return cpq::launched(cpq::launch_qmm(cmds->stream, q, x, y, (int)m, (int)n, (int)k),
+                       "affine_qmm_t launch");
+}
+
+cpq_status cpq_affine_dequantize(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q,
+                                 size_t w_q_len, const void* scales, size_t scales_len,
+                                 const void* biases, size_t biases_len, void* out,
+                                 size_t out_len, uint32_t group_size, uint32_t bits) {
+  if (!cmds) return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_dequantize: NULL command session");
+  cpq_status st = cpq_check_dequantize_args(dtype, w_q_len, scales_len, biases_len, out_len,
+                                            group_size, bits);
+  if (st != CPQ_OK) return st;
+  if (out_len == 0) return CPQ_OK;
+  st = cpq::check_ptrs("affine_dequantize", w_q, scales, biases, out, out);
+  if (st != CPQ_OK) return st;
+  cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
+  return cpq::launched(cpq::launch_dequantize(cmds->stream, q, out, out_len),
+                       "affine_dequantize launch");
+}
+
+cpq_status cpq_affine_gather_qmm(cpq_commands* cmds, cpq_dtype dtype, const void* x,
+                                 size_t x_rows, const uint32_t* w_q, size_t w_q_len,
+                                 const void* scales, size_t scales_len, const void* biases,
+                                 size_t biases_len, const uint32_t* lhs_indices,
+                                 const uint32_t* rhs_indices, size_t n_rows, void* y,
+                                 size_t y_len, size_t n_experts, size_t n, size_t k,
+                                 uint32_t group_size, uint32_t bits, int sorted_indices) {
+  if (!cmds) return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_gather_qmm: NULL command session");
+  cpq_status st = cpq_check_gather_args(dtype, x_rows, w_q_len, scales_len, biases_len,
+                                        lhs_indices != nullptr, n_rows, y_len, n_experts, n, k,
+                                        group_size, bits);
+  if (st != CPQ_OK) return st;
+  if (n_rows == 0) return CPQ_OK;
+  if (!rhs_indices) return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_gather_qmm: rhs_indices is NULL");
+  st = cpq::check_ptrs("affine_gather_qmm", w_q, scales, biases, x, y);
+  if (st != CPQ_OK) return st;
+  if (x_rows == 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_gather_qmm: x has no rows but lhs_indices select some");
+  cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
+  return cpq::launched(cpq::launch_gather_qmm(cmds->stream, q, x, (int)x_rows, lhs_indices,
+                                              rhs_indices, (int)n_rows, y, (int)n_experts, (int)n,
+                                              (int)k, sorted_indices != 0, cmds->status),
+                       "affine_gather_qmm launch");
+}
+
+cpq_status cpq_quantized_matmul(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q,
+                                size_t w_q_len, const void* scales, size_t scales_len,
+                                const void* biases, size_t biases_len, const void* x, size_t x_len,
+                                size_t x_alloc_bytes, void* y, size_t m, size_t n,
+                                size_t k_physical, uint32_t group_size, uint32_t bits) {
+  if (!cmds) return fail(CPQ_ERR_INVALID_ARGUMENT, "quantized_matmul: NULL command session");
+  if (m == 0) return fail(CPQ_ERR_INVALID_ARGUMENT, "quantized_matmul: activation has no rows");
+  if (m == 1) {
+    // eval.rs:1360-1372: M == 1 -> qmv (K-padded activations allowed).
+    return cpq_affine_qmv(cmds, dtype, w_q, w_q_len, scales, scales_len, biases, biases_len, x,
+                          x_alloc_bytes, y, n, k_physical, group_size, bits);
+  }
+  // eval.rs:1377-1390: M > 1 -> qmm_t contract (x.len() == M*K, N % 32 == 0);
+  // a K-padded weight self-rejects here because x_len == M*k_logical.
+  if (x_alloc_bytes < x_len * cpq::dtype_size(dtype))
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "quantized_matmul: x allocation smaller than x_len");
+  size_t mn;
+  if (!cpq::mul_ok(m, n, &mn)) return fail(CPQ_ERR_INVALID_ARGUMENT, "quantized_matmul: M*N overflows usize");
+  cpq_status st = cpq_check_qmm_args(dtype, w_q_len, scales_len, biases_len, x_len, mn, m, n,
+                                     k_physical, group_size, bits);
+  if (st != CPQ_OK) return st;
+  st = cpq::check_ptrs("quantized_matmul", w_q, scales, biases, x, y);
+  if (st != CPQ_OK) return st;
+  cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
+  if ((long)m <= cpq::skinny_max_m(q, (int)n, (int)k_physical))
+    return cpq::launched(cpq::launch_qmm_skinny(cmds->stream, q, x, y, (int)m, (int)n, (int)k_physical),
+                         "quantized_matmul (small-M) launch");
+  return cpq::launched(cpq::launch_qmm(cmds->stream, q, x, y, (int)m, (int)n, (int)k_physical),
+                       "quantized_matmul (prefill) launch");
+}
+
+}  // extern "C"

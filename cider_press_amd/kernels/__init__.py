@@ -1,0 +1,231 @@
+"""Kernel dispatch and buffer layer (mirror of the reference's cider-press-kernels
+crate, crates/cider-press-kernels/src/lib.rs:35-40), backed by libcpq.so.
+
+    Device.system_default()        -> device.rs:77
+    device.alloc_buffer / upload   -> device.rs:167-233 (512-B rounding, zeroed slack)
+    device.commands()              -> device.rs:319 (one in-order HIP stream)
+    Commands.commit / wait         -> commands.rs:349-419
+    KernelLibrary.quantized(dev)   -> library.rs:230 (kernels are compiled ahead of time)
+    kernels.{qmv,qmm,dequantize,gather}.*  -> kernels/{qmv,qmm,dequantize}.rs
+
+Buffers are typed views over device memory; 16-bit float buffers hold raw
+uint16 bit patterns on the host side (numpy has no bfloat16).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from .. import _lib
+from .._lib import (BufferAllocation, BufferTooLarge, CommandBufferFailed, Error, HipApi,  # noqa: F401
+                    InvalidArgument, KernelNotFound, NoDevice)
+
+_NP = {"u32": np.uint32, "bf16": np.uint16, "f16": np.uint16, "u16": np.uint16, "u8": np.uint8,
+       "f32": np.float32}
+_SIZE = {"u32": 4, "bf16": 2, "f16": 2, "u16": 2, "u8": 1, "f32": 4}
+
+
+class Device:
+    def __init__(self, handle):
+        self._h = handle
+        self._lib = _lib.lib()
+
+    @staticmethod
+    def system_default() -> "Device":
+        L = _lib.lib()
+        h = ctypes.c_void_p()
+        _lib.check(L.cpq_device_system_default(ctypes.byref(h)))
+        return Device(h)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def info(self) -> dict:
+        name = ctypes.create_string_buffer(256)
+        cus, clk = ctypes.c_int(), ctypes.c_int()
+        _lib.check(self._lib.cpq_device_info(self._h, name, 256, ctypes.byref(cus), ctypes.byref(clk)))
+        return {"name": name.value.decode(), "cu_count": cus.value, "clock_khz": clk.value}
+
+    def alloc_buffer(self, length: int, dtype: str) -> "Buffer":
+        ptr, alloc = ctypes.c_void_p(), ctypes.c_size_t()
+        _lib.check(self._lib.cpq_alloc_buffer(self._h, length * _SIZE[dtype], ctypes.byref(ptr),
+                                              ctypes.byref(alloc)))
+        return Buffer(self, ptr.value, length, dtype, alloc.value)
+
+    def upload(self, array: np.ndarray, dtype: str) -> "Buffer":
+        a = np.ascontiguousarray(array, dtype=_NP[dtype])
+        ptr, alloc = ctypes.c_void_p(), ctypes.c_size_t()
+        _lib.check(self._lib.cpq_upload(self._h, a.ctypes.data_as(ctypes.c_void_p), a.nbytes,
+                                        ctypes.byref(ptr), ctypes.byref(alloc)))
+        return Buffer(self, ptr.value, a.size, dtype, alloc.value)
+
+    def commands(self) -> "Commands":
+        h = ctypes.c_void_p()
+        _lib.check(self._lib.cpq_commands_create(self._h, ctypes.byref(h)))
+        return Commands(self, h)
+
+    def wrap_stream(self, hip_stream: int) -> "Commands":
+        h = ctypes.c_void_p()
+        _lib.check(self._lib.cpq_commands_wrap_stream(self._h, ctypes.c_void_p(hip_stream), ctypes.byref(h)))
+        return Commands(self, h)
+
+    def __del__(self):
+        if getattr(self, "_h", None) and self._lib is not None:
+            self._lib.cpq_device_release(self._h)
+            self._h = None
+
+
+class Buffer:
+    """A device allocation (Buffer<T>, buffer.rs:62-199)."""
+
+    def __init__(self, device: Device, ptr: int, length: int, dtype: str, alloc_len: int):
+        self.device = device
+        self.ptr = ptr
+        self._len = length
+        self.dtype = dtype
+        self.alloc_len = alloc_len  # Buffer::metal_alloc_len analogue
+
+    def __len__(self):
+        return self._len
+
+    @property
+    def byte_len(self) -> int:
+        return self._len * _SIZE[self.dtype]
+
+    def to_numpy(self) -> np.ndarray:
+        """Host copy (Buffer::as_slice after a wait)."""
+        out = np.empty(self._len, _NP[self.dtype])
+        _lib.check(_lib.lib().cpq_read_buffer(self.device.handle, ctypes.c_void_p(self.ptr),
+                                              out.ctypes.data_as(ctypes.c_void_p), out.nbytes))
+        return out
+
+    def read_bytes(self, nbytes: int) -> np.ndarray:
+        """Raw bytes of the allocation, including the rounded slack."""
+        out = np.empty(nbytes, np.uint8)
+        _lib.check(_lib.lib().cpq_read_buffer(self.device.handle, ctypes.c_void_p(self.ptr),
+                                              out.ctypes.data_as(ctypes.c_void_p), nbytes))
+        return out
+
+    def write(self, array: np.ndarray) -> None:
+        a = np.ascontiguousarray(array, dtype=_NP[self.dtype])
+        if a.size != self._len:
+            raise ValueError(f"write: {a.size} elements into a buffer of {self._len}")
+        _lib.check(_lib.lib().cpq_write_buffer(self.device.handle, ctypes.c_void_p(self.ptr),
+                                               a.ctypes.data_as(ctypes.c_void_p), a.nbytes))
+
+    def reinterpret_as(self, dtype: str) -> "Buffer":
+        """Same allocation viewed with another element type (buffer.rs reinterpret_as)."""
+        n = self.byte_len // _SIZE[dtype]
+        view = Buffer(self.device, self.ptr, n, dtype, self.alloc_len)
+        view._owner = self
+        return view
+
+    def __del__(self):
+        if getattr(self, "_owner", None) is None and getattr(self, "ptr", None):
+            L = _lib._lib
+            if L is not None:
+                L.cpq_free_buffer(self.device.handle, ctypes.c_void_p(self.ptr))
+            self.ptr = None
+
+
+class Commands:
+    """A command session on one HIP stream (commands.rs)."""
+
+    def __init__(self, device: Device, handle):
+        self.device = device
+        self._h = handle
+        self._lib = _lib.lib()
+
+    @property
+    def handle(self):
+        return self._h
+
+    @property
+    def stream(self) -> int:
+        return self._lib.cpq_commands_stream(self._h) or 0
+
+    def commit(self) -> "Commands":
+        _lib.check(self._lib.cpq_commands_commit(self._h))
+        return self
+
+    def wait(self) -> None:
+        _lib.check(self._lib.cpq_commands_wait(self._h))
+
+    def commit_and_wait(self) -> None:
+        _lib.check(self._lib.cpq_commands_commit_and_wait(self._h))
+
+    def begin_capture(self) -> None:
+        """Record (not run) everything encoded until end_capture into a HIP graph."""
+        _lib.check(self._lib.cpq_commands_begin_capture(self._h))
+
+    def end_capture(self) -> "Graph":
+        g = ctypes.c_void_p()
+        _lib.check(self._lib.cpq_commands_end_capture(self._h, ctypes.byref(g)))
+        return Graph(g)
+
+    def __del__(self):
+        if getattr(self, "_h", None) and self._lib is not None:
+            self._lib.cpq_commands_release(self._h)
+            self._h = None
+
+
+class Graph:
+    """An instantiated HIP graph captured from a session."""
+
+    def __init__(self, handle):
+        self._h = handle
+        self._lib = _lib.lib()
+
+    def launch(self, cmds: Commands) -> None:
+        _lib.check(self._lib.cpq_graph_launch(self._h, cmds.handle))
+
+    def __del__(self):
+        if getattr(self, "_h", None) and self._lib is not None:
+            self._lib.cpq_graph_release(self._h)
+            self._h = None
+
+
+class Event:
+    """GPU timestamp on a session's stream (replaces the reference's GpuSampler)."""
+
+    def __init__(self):
+        self._lib = _lib.lib()
+        self._h = ctypes.c_void_p()
+        _lib.check(self._lib.cpq_event_create(ctypes.byref(self._h)))
+
+    def record(self, cmds: Commands) -> None:
+        _lib.check(self._lib.cpq_event_record(self._h, cmds.handle))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float()
+        _lib.check(self._lib.cpq_event_elapsed_ms(self._h, end._h, ctypes.byref(ms)))
+        return float(ms.value)
+
+    def __del__(self):
+        if getattr(self, "_h", None) and self._lib is not None:
+            self._lib.cpq_event_release(self._h)
+            self._h = None
+
+
+class KernelLibrary:
+    """The quantized kernel catalogue (library.rs:230); kernels are built ahead of time."""
+
+    def __init__(self, device: Device):
+        self.device = device
+
+    @staticmethod
+    def quantized(device: Device) -> "KernelLibrary":
+        return KernelLibrary(device)
+
+    @staticmethod
+    def available(dtype: str, group_size: int, bits: int) -> bool:
+        return bool(_lib.lib().cpq_kernel_available(_lib.DTYPES[dtype], group_size, bits))
+
+
+def _ptr(buf) -> ctypes.c_void_p:
+    return ctypes.c_void_p(None if buf is None else buf.ptr)
+
+
+from . import dequantize, gather, qmm, qmv  # noqa: E402,F401

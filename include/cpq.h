@@ -1,0 +1,256 @@
+/*
+ * cpq.h -- C ABI of the MI355X (gfx950) affine group-quantized matmul library
+ * (libcpq.so).  Drop-in boundary for the reference's quantized-matmul path:
+ * the kernels crate's dispatch/buffer layer and op API
+ * (crates/cider-press-kernels/src/{device,buffer,commands,error}.rs and
+ * kernels/{qmv,qmm,dequantize}.rs) and the runtime's QuantizedMatMul node
+ * (crates/cider-press-runtime/src/{quantization,quantized,tensor,eval}.rs).
+ *
+ * Conventions
+ *  - Plain pointers and element counts; no framework types.  16-bit floats
+ *    are passed as `const void*` and interpreted per `cpq_dtype`.
+ *  - Ops ENCODE ONLY: they validate, enqueue on the session's HIP stream and
+ *    return.  Nothing synchronises until cpq_commands_wait / commit_and_wait
+ *    (reference: kernels/mod.rs:1-9 "functions never commit").
+ *  - Every shape/divisibility violation returns CPQ_ERR_INVALID_ARGUMENT
+ *    before any launch; an unsupported (dtype, group_size, bits) returns
+ *    CPQ_ERR_KERNEL_NOT_FOUND; a failed stream surfaces at wait as
+ *    CPQ_ERR_COMMAND_BUFFER_FAILED.  The message of the last failure on the
+ *    calling thread is cpq_last_error_message().
+ *  - Caller owns all device buffers.  Quantized weights are never written.
+ *  - Thread safety: one thread drives a given cpq_commands at a time; the
+ *    library itself holds no mutable global state besides per-thread error
+ *    text and the per-device kernel property cache.
+ */
+#ifndef CPQ_H
+#define CPQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error classes; mirror cider_press_kernels::Error (error.rs:15-70). */
+typedef enum cpq_status {
+  CPQ_OK = 0,
+  CPQ_ERR_NO_DEVICE = 1,             /* Error::NoDevice            error.rs:21-23 */
+  CPQ_ERR_KERNEL_NOT_FOUND = 2,      /* Error::KernelNotFound      error.rs:30-34 */
+  CPQ_ERR_BUFFER_ALLOCATION = 3,     /* Error::BufferAllocation    error.rs:40-42 */
+  CPQ_ERR_BUFFER_TOO_LARGE = 4,      /* Error::BufferTooLarge      error.rs:44-48 */
+  CPQ_ERR_INVALID_ARGUMENT = 5,      /* Error::InvalidArgument     error.rs:56-61 */
+  CPQ_ERR_COMMAND_BUFFER_FAILED = 6, /* Error::CommandBufferFailed error.rs:63-69 */
+  CPQ_ERR_HIP_API = 7                /* Error::AppleApi analogue   error.rs:50-54 */
+} cpq_status;
+
+/* Activation / scale / bias / output element type (T). */
+typedef enum cpq_dtype {
+  CPQ_DTYPE_F32 = 0, /* accepted by validators; no f32 kernels are built */
+  CPQ_DTYPE_F16 = 1,
+  CPQ_DTYPE_BF16 = 2
+} cpq_dtype;
+
+typedef struct cpq_device cpq_device;
+typedef struct cpq_commands cpq_commands;
+typedef struct cpq_event cpq_event;
+typedef struct cpq_qweight cpq_qweight;
+typedef struct cpq_tensor cpq_tensor;
+
+/* ------------------------------------------------------------------ */
+/* Errors and version                                                   */
+/* ------------------------------------------------------------------ */
+
+/* Text of the last non-OK status returned on this thread ("" if none). */
+const char* cpq_last_error_message(void);
+const char* cpq_version(void);
+
+/* ------------------------------------------------------------------ */
+/* Device and buffers (kernels/src/device.rs, buffer.rs)                */
+/* ------------------------------------------------------------------ */
+
+/* Device::system_default (device.rs:77): HIP device 0.  CPQ_ERR_NO_DEVICE if absent. */
+cpq_status cpq_device_system_default(cpq_device** out);
+void cpq_device_release(cpq_device* dev);
+/* Marketing name, compute-unit count and peak clock (kHz) of the device. */
+cpq_status cpq_device_info(cpq_device* dev, char* name, size_t name_cap, int* cu_count,
+                           int* clock_khz);
+
+/* Device::alloc_buffer (device.rs:167-228): allocation rounded up to 512 B,
+ * the slack past byte_len zeroed (the K-padding contract of qmv.rs:95-124).
+ * *out_alloc_len receives the rounded length (Buffer::metal_alloc_len). */
+cpq_status cpq_alloc_buffer(cpq_device* dev, size_t byte_len, void** out_ptr,
+                            size_t* out_alloc_len);
+/* Device::upload (device.rs:233): alloc_buffer + synchronous host->device copy. */
+cpq_status cpq_upload(cpq_device* dev, const void* host, size_t byte_len, void** out_ptr,
+                      size_t* out_alloc_len);
+cpq_status cpq_free_buffer(cpq_device* dev, void* ptr);
+/* Synchronous copies (Buffer::as_slice / as_mut_slice after a wait, buffer.rs:176-199). */
+cpq_status cpq_read_buffer(cpq_device* dev, const void* dev_ptr, void* host, size_t byte_len);
+cpq_status cpq_write_buffer(cpq_device* dev, void* dev_ptr, const void* host, size_t byte_len);
+
+/* ------------------------------------------------------------------ */
+/* Command sessions (kernels/src/commands.rs): one in-order HIP stream   */
+/* ------------------------------------------------------------------ */
+
+/* Device::commands (device.rs:319): a new session on its own HIP stream. */
+cpq_status cpq_commands_create(cpq_device* dev, cpq_commands** out);
+/* Wrap a caller-owned hipStream_t (e.g. a framework's current stream). */
+cpq_status cpq_commands_wrap_stream(cpq_device* dev, void* hip_stream, cpq_commands** out);
+void* cpq_commands_stream(cpq_commands* cmds);
+/* Commands::commit (commands.rs:349-359): work is already submitted on HIP; a no-op flush. */
+cpq_status cpq_commands_commit(cpq_commands* cmds);
+/* CommandsInFlight::wait (commands.rs:416-419): hipStreamSynchronize; a stream
+ * failure maps to CPQ_ERR_COMMAND_BUFFER_FAILED (commands.rs:381-400). */
+cpq_status cpq_commands_wait(cpq_commands* cmds);
+cpq_status cpq_commands_commit_and_wait(cpq_commands* cmds);
+void cpq_commands_release(cpq_commands* cmds);
+
+/* HIP graph capture of a session's stream: everything encoded between begin
+ * and end is recorded (not run) and replayed by cpq_graph_launch.  No op of
+ * this library records a memset, so captured graphs replay identically.  No
+ * counterpart in the reference (Metal command buffers are re-encoded per
+ * call); used for decode loops and for launch-overhead-free timing. */
+typedef struct cpq_graph cpq_graph;
+cpq_status cpq_commands_begin_capture(cpq_commands* cmds);
+cpq_status cpq_commands_end_capture(cpq_commands* cmds, cpq_graph** out);
+cpq_status cpq_graph_launch(cpq_graph* graph, cpq_commands* cmds);
+void cpq_graph_release(cpq_graph* graph);
+
+/* GPU timing on a session's stream (replaces GpuSampler, gpu_sampler.rs). */
+cpq_status cpq_event_create(cpq_event** out);
+cpq_status cpq_event_record(cpq_event* ev, cpq_commands* cmds);
+cpq_status cpq_event_elapsed_ms(cpq_event* start, cpq_event* end, float* out_ms);
+void cpq_event_release(cpq_event* ev);
+
+/* ------------------------------------------------------------------ */
+/* Quantization descriptor (runtime/src/quantization.rs:43-153)          */
+/* ------------------------------------------------------------------ */
+
+/* Quantization::validate (quantization.rs:86-106): bits in {2,3,4,5,6,8},
+ * group_size a positive power of two, group_size*bits % 32 == 0. */
+cpq_status cpq_quantization_validate(uint32_t bits, uint32_t group_size);
+/* Quantization::packed_word_count (quantization.rs:121-141). */
+cpq_status cpq_packed_word_count(uint32_t bits, uint32_t group_size, size_t scalar_count,
+                                 size_t* out);
+/* Quantization::group_count (quantization.rs:145-153). */
+cpq_status cpq_group_count(uint32_t bits, uint32_t group_size, size_t scalar_count,
+                           size_t* out);
+/* KernelLibrary::pipeline lookup (library.rs:264-286): 1 if a kernel for
+ * (dtype, group_size, bits) is built, else 0. */
+int cpq_kernel_available(cpq_dtype dtype, uint32_t group_size, uint32_t bits);
+
+/* ------------------------------------------------------------------ */
+/* Ops (kernels/src/kernels/{qmv,qmm,dequantize}.rs)                     */
+/* ------------------------------------------------------------------ */
+
+/* affine_qmv_bf16 (qmv.rs:77-205), any T: y[N] = x . dequant(w_q)^T for one
+ * activation row.  in_vec_size is the PHYSICAL K of the weight; x may be a
+ * K-padded activation whose allocation (x_alloc_bytes) covers K*sizeof(T)
+ * with a zeroed tail.  N = y_len.  w_q_len = N*K*bits/32,
+ * scales_len = biases_len = N*K/group_size. */
+cpq_status cpq_affine_qmv(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q,
+                          size_t w_q_len, const void* scales, size_t scales_len,
+                          const void* biases, size_t biases_len, const void* x,
+                          size_t x_alloc_bytes, void* y, size_t y_len, size_t in_vec_size,
+                          uint32_t group_size, uint32_t bits);
+
+/* affine_qmm_t_bf16 (qmm.rs:66-220), any T: Y[M,N] = X[M,K] . dequant(W[N,K])^T.
+ * N % 32 == 0 is required as in the reference's aligned variant (qmm.rs:101-106). */
+cpq_status cpq_affine_qmm_t(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q,
+                            size_t w_q_len, const void* scales, size_t scales_len,
+                            const void* biases, size_t biases_len, const void* x, size_t x_len,
+                            void* y, size_t y_len, size_t m, size_t n, size_t k,
+                            uint32_t group_size, uint32_t bits);
+
+/* affine_dequantize_bf16_gs64_b4 (dequantize.rs:58-137), any (T, gs, bits):
+ * out[i] = RNE_T(fmaf(scale, q_i, bias)) for out_len elements laid out as
+ * consecutive groups of group_size.  out_len == 0 is a no-op. */
+cpq_status cpq_affine_dequantize(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q,
+                                 size_t w_q_len, const void* scales, size_t scales_len,
+                                 const void* biases, size_t biases_len, void* out,
+                                 size_t out_len, uint32_t group_size, uint32_t bits);
+
+/* Routed-expert quantized matmul.  No wired counterpart in the reference: its
+ * semantics follow the vendored MSL affine_gather_qmm_t / affine_gather_qmm_rhs
+ * (kernels-mlx/.../quantized.h:2092-2172, 2242-2436):
+ *   Y[r, :] = X[lhs_indices[r], :] . dequant(W[rhs_indices[r]])^T,  r < n_rows.
+ * W holds n_experts matrices of [N, K] back to back (scales/biases likewise).
+ * lhs_indices may be NULL (row r reads X row r; X then has n_rows rows).
+ * rhs_indices need not be sorted; sorted_indices=1 promises ascending order
+ * (enables the run-walking schedule of gather_qmm_rhs).  Every index is
+ * checked on the device: out-of-range entries produce a zero row and the
+ * count of such rows is reported by the next cpq_commands_wait as
+ * CPQ_ERR_INVALID_ARGUMENT. */
+cpq_status cpq_affine_gather_qmm(cpq_commands* cmds, cpq_dtype dtype, const void* x,
+                                 size_t x_rows, const uint32_t* w_q, size_t w_q_len,
+                                 const void* scales, size_t scales_len, const void* biases,
+                                 size_t biases_len, const uint32_t* lhs_indices,
+                                 const uint32_t* rhs_indices, size_t n_rows, void* y,
+                                 size_t y_len, size_t n_experts, size_t n, size_t k,
+                                 uint32_t group_size, uint32_t bits, int sorted_indices);
+
+/* dispatch_quantized_matmul (runtime/src/eval.rs:1293-1394): Y[M,N] for an
+ * activation of M rows against a [N, k_physical] weight; routes by M to the
+ * decode (M==1), small-batch, or prefill kernel.  x_len is the activation's
+ * logical element count and x_alloc_bytes its allocation: M==1 follows the
+ * qmv contract (K-padded activations allowed when the allocation covers
+ * k_physical), M>1 the qmm_t contract (x_len == M*k_physical, N % 32 == 0). */
+cpq_status cpq_quantized_matmul(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q,
+                                size_t w_q_len, const void* scales, size_t scales_len,
+                                const void* biases, size_t biases_len, const void* x, size_t x_len,
+                                size_t x_alloc_bytes, void* y, size_t m, size_t n,
+                                size_t k_physical, uint32_t group_size, uint32_t bits);
+
+/* Host-only argument validators used by the ops above (callable without a GPU). */
+cpq_status cpq_check_qmv_args(cpq_dtype dtype, size_t w_q_len, size_t scales_len,
+                              size_t biases_len, size_t x_alloc_bytes, size_t y_len,
+                              size_t in_vec_size, uint32_t group_size, uint32_t bits);
+cpq_status cpq_check_qmm_args(cpq_dtype dtype, size_t w_q_len, size_t scales_len,
+                              size_t biases_len, size_t x_len, size_t y_len, size_t m, size_t n,
+                              size_t k, uint32_t group_size, uint32_t bits);
+cpq_status cpq_check_dequantize_args(cpq_dtype dtype, size_t w_q_len, size_t scales_len,
+                                     size_t biases_len, size_t out_len, uint32_t group_size,
+                                     uint32_t bits);
+cpq_status cpq_check_gather_args(cpq_dtype dtype, size_t x_rows, size_t w_q_len,
+                                 size_t scales_len, size_t biases_len, int has_lhs,
+                                 size_t n_rows, size_t y_len, size_t n_experts, size_t n,
+                                 size_t k, uint32_t group_size, uint32_t bits);
+
+/* ------------------------------------------------------------------ */
+/* Runtime node (runtime/src/{quantized,tensor,eval}.rs)                 */
+/* ------------------------------------------------------------------ */
+
+/* QuantizedWeight::from_bytes / from_bytes_k_padded (quantized.rs:59-125):
+ * logical shape [n, k_logical] stored as physical [n, k_physical];
+ * k_logical == k_physical for an unpadded weight.  Byte lengths are checked. */
+cpq_status cpq_qweight_from_bytes(cpq_device* dev, cpq_dtype dtype, size_t n,
+                                  size_t k_physical, size_t k_logical, uint32_t bits,
+                                  uint32_t group_size, const void* weights, size_t weights_bytes,
+                                  const void* scales, size_t scales_bytes, const void* biases,
+                                  size_t biases_bytes, cpq_qweight** out);
+void cpq_qweight_release(cpq_qweight* w);
+
+/* A dense leaf tensor uploaded from host memory (contiguous, row-major). */
+cpq_status cpq_tensor_from_host(cpq_device* dev, cpq_dtype dtype, const size_t* dims,
+                                size_t ndim, const void* data, cpq_tensor** out);
+/* Tensor::quantized_matmul (tensor.rs:2064-2171): records a lazy
+ * QuantizedMatMul node; no GPU work.  transpose must be 1. */
+cpq_status cpq_tensor_quantized_matmul(cpq_tensor* x, cpq_qweight* w, int transpose,
+                                       cpq_tensor** out);
+/* Tensor::dequantize_affine (tensor.rs:1558-1637): lazy Dequantize node producing
+ * the dense [n, k_physical] weight. */
+cpq_status cpq_tensor_dequantize(cpq_qweight* w, cpq_tensor** out);
+/* Tensor::eval (tensor.rs:2681): encodes every pending node on the device's
+ * session, commits and waits. */
+cpq_status cpq_tensor_eval(cpq_tensor* t);
+cpq_status cpq_tensor_shape(cpq_tensor* t, size_t* dims, size_t cap, size_t* ndim);
+/* Host copy of an evaluated tensor (Tensor::cpu_slice). */
+cpq_status cpq_tensor_read(cpq_tensor* t, void* host, size_t byte_len);
+void cpq_tensor_release(cpq_tensor* t);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CPQ_H */
