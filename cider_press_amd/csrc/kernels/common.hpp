@@ -173,6 +173,147 @@ __device__ __forceinline__ void load_chunk(const uint32_t* __restrict__ row, siz
   }
 }
 
+// ---------------------------------------------------------------------------
+// Interleaved-slice dequantization (MFMA B operands).
+//
+// A "slice" is 8 consecutive elements of a chunk (one word at 4-bit, two at
+// 8-bit), i.e. one MFMA operand of 8 elements per lane.  The matrix cores
+// only need A and B to agree on which k each operand slot holds, so the
+// weights are produced in the order that is cheapest to build and the
+// activations are permuted once (when staged) to the same order:
+//   4-bit and generic widths: slot pairs (e0,e4) (e1,e5) (e2,e6) (e3,e7)
+//   8-bit:                    slot pairs (e0,e2) (e1,e3) (e4,e6) (e5,e7)
+//
+// Fast path (4/8-bit): a nibble or byte is dropped into the mantissa of an
+// f16 "magic" 1024 (bit pattern 0x6400 | q), giving 1024+q exactly (or
+// 1024+16q for a nibble left in place in the high half of a byte); one
+// v_fma_mix_f32 then computes s*(1024+q) + (b - 1024*s) == fmaf(s, q, b)
+// with a single rounding -- exact whenever c0 = b - 1024*s (and, at 4-bit,
+// c1 = b - 64*s) is itself exact in fp32.  fast_ok() checks that per group;
+// groups that fail take the slow path (explicit byte conversions), which
+// produces the same bits.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c));
+  return r;
+}
+
+__device__ __forceinline__ float f16lo(uint32_t p) {
+  return (float)__builtin_bit_cast(f16x2, p).x;
+}
+__device__ __forceinline__ float f16hi(uint32_t p) {
+  return (float)__builtin_bit_cast(f16x2, p).y;
+}
+
+// Significand width of T (bf16: 8, f16: 11).
+template <typename TT>
+struct Sig;
+template <>
+struct Sig<BF16> {
+  static constexpr int P = 8;
+};
+template <>
+struct Sig<F16> {
+  static constexpr int P = 11;
+};
+
+// True when c0 = b - 1024*s and c1 = b - 64*s are exact in fp32 and no
+// intermediate can be subnormal: then the fast path equals fmaf(s, q, b).
+template <typename TT>
+__device__ __forceinline__ bool fast_ok(float s, float b) {
+  const uint32_t su = __float_as_uint(s), bu = __float_as_uint(b);
+  const int es = (int)((su >> 23) & 0xffu), eb = (int)((bu >> 23) & 0xffu);
+  if ((su & 0x7fffffffu) == 0u) return (bu & 0x7fffffffu) == 0u || (eb >= 27 && eb < 255);
+  if (es < 27 || es > 240) return false;      // |s| outside [2^-100, 2^113]
+  if ((bu & 0x7fffffffu) == 0u) return true;  // b == 0: c0 = -1024 s, c1 = -64 s
+  if (eb < 27 || eb == 255) return false;
+  constexpr int span = 23 - Sig<TT>::P;
+  const int d0 = eb - (es + 10), d1 = eb - (es + 6);
+  return d0 <= span && d0 >= -span && d1 <= span && d1 >= -span;
+}
+
+// Natural 16-byte activation slice -> interleaved slot order of BITS.
+template <int BITS>
+__device__ __forceinline__ u32x4 interleave_x(u32x4 v) {
+  if constexpr (BITS == 8) {
+    return u32x4{__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.y, v.x, 0x07060302u),
+                 __builtin_amdgcn_perm(v.w, v.z, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u)};
+  } else {
+    return u32x4{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                 __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
+  }
+}
+
+// Slice I (0..3) of a 32-element chunk held in `w` (BITS words), dequantized
+// to 4 packed T pairs in the interleaved slot order.
+template <typename TT, int BITS, bool FAST, int I>
+__device__ __forceinline__ u32x4 dequant_slice(const uint32_t* w, float s, float s16, float b, float c0,
+                                               float c1) {
+  if constexpr (BITS == 4 && FAST) {
+    const uint32_t M = 0x64006400u;
+    const uint32_t word = w[I];
+    const uint32_t w8 = word >> 8;
+    const uint32_t p0 = and_or(word, 0x000F000Fu, M);  // (1024+q0, 1024+q4)
+    const uint32_t p1 = and_or(word, 0x00F000F0u, M);  // (1024+16q1, 1024+16q5)
+    const uint32_t p2 = and_or(w8, 0x000F000Fu, M);    // (1024+q2, 1024+q6)
+    const uint32_t p3 = and_or(w8, 0x00F000F0u, M);    // (1024+16q3, 1024+16q7)
+    return u32x4{TT::pack2(fmaf(s, f16lo(p0), c0), fmaf(s, f16hi(p0), c0)),
+                 TT::pack2(fmaf(s16, f16lo(p1), c1), fmaf(s16, f16hi(p1), c1)),
+                 TT::pack2(fmaf(s, f16lo(p2), c0), fmaf(s, f16hi(p2), c0)),
+                 TT::pack2(fmaf(s16, f16lo(p3), c1), fmaf(s16, f16hi(p3), c1))};
+  } else if constexpr (BITS == 8 && FAST) {
+    const uint32_t M = 0x64646464u;
+    const uint32_t w0 = w[2 * I], w1 = w[2 * I + 1];
+    const uint32_t p0 = __builtin_amdgcn_perm(M, w0, 0x04020400u);  // (1024+e0, 1024+e2)
+    const uint32_t p1 = __builtin_amdgcn_perm(M, w0, 0x04030401u);  // (1024+e1, 1024+e3)
+    const uint32_t p2 = __builtin_amdgcn_perm(M, w1, 0x04020400u);  // (1024+e4, 1024+e6)
+    const uint32_t p3 = __builtin_amdgcn_perm(M, w1, 0x04030401u);  // (1024+e5, 1024+e7)
+    return u32x4{TT::pack2(fmaf(s, f16lo(p0), c0), fmaf(s, f16hi(p0), c0)),
+                 TT::pack2(fmaf(s, f16lo(p1), c0), fmaf(s, f16hi(p1), c0)),
+                 TT::pack2(fmaf(s, f16lo(p2), c0), fmaf(s, f16hi(p2), c0)),
+                 TT::pack2(fmaf(s, f16lo(p3), c0), fmaf(s, f16hi(p3), c0))};
+  } else if constexpr (BITS == 4) {
+    const uint32_t word = w[I];
+    const uint32_t lo = opaque(word & 0x0F0F0F0Fu);  // q0 q2 q4 q6
+    const uint32_t hi = opaque(word & 0xF0F0F0F0u);  // 16q1 16q3 16q5 16q7
+    return u32x4{TT::pack2(fmaf(s, ubyte_f32<0>(lo), b), fmaf(s, ubyte_f32<2>(lo), b)),
+                 TT::pack2(fmaf(s16, ubyte_f32<0>(hi), b), fmaf(s16, ubyte_f32<2>(hi), b)),
+                 TT::pack2(fmaf(s, ubyte_f32<1>(lo), b), fmaf(s, ubyte_f32<3>(lo), b)),
+                 TT::pack2(fmaf(s16, ubyte_f32<1>(hi), b), fmaf(s16, ubyte_f32<3>(hi), b))};
+  } else if constexpr (BITS == 8) {
+    const uint32_t w0 = w[2 * I], w1 = w[2 * I + 1];
+    return u32x4{TT::pack2(fmaf(s, ubyte_f32<0>(w0), b), fmaf(s, ubyte_f32<2>(w0), b)),
+                 TT::pack2(fmaf(s, ubyte_f32<1>(w0), b), fmaf(s, ubyte_f32<3>(w0), b)),
+                 TT::pack2(fmaf(s, ubyte_f32<0>(w1), b), fmaf(s, ubyte_f32<2>(w1), b)),
+                 TT::pack2(fmaf(s, ubyte_f32<1>(w1), b), fmaf(s, ubyte_f32<3>(w1), b))};
+  } else {
+    // generic widths: explicit extraction, (e_j, e_{j+4}) pairs
+    return u32x4{TT::pack2(fmaf(s, (float)chunk_elem<BITS, 8 * I + 0>(w), b), fmaf(s, (float)chunk_elem<BITS, 8 * I + 4>(w), b)),
+                 TT::pack2(fmaf(s, (float)chunk_elem<BITS, 8 * I + 1>(w), b), fmaf(s, (float)chunk_elem<BITS, 8 * I + 5>(w), b)),
+                 TT::pack2(fmaf(s, (float)chunk_elem<BITS, 8 * I + 2>(w), b), fmaf(s, (float)chunk_elem<BITS, 8 * I + 6>(w), b)),
+                 TT::pack2(fmaf(s, (float)chunk_elem<BITS, 8 * I + 3>(w), b), fmaf(s, (float)chunk_elem<BITS, 8 * I + 7>(w), b))};
+  }
+}
+
+template <typename TT>
+struct Mfma16;
+template <>
+struct Mfma16<BF16> {
+  static __device__ __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma16<F16> {
+  static __device__ __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
 // Wave64 sum via DPP-friendly butterfly.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

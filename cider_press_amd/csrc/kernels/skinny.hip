@@ -31,23 +31,6 @@ namespace {
 
 using namespace dev;
 
-template <typename TT>
-struct Mfma16;
-template <>
-struct Mfma16<BF16> {
-  static __device__ __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-};
-template <>
-struct Mfma16<F16> {
-  static __device__ __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-};
-
 constexpr int kWaves = 4;
 constexpr int kMaxMB = 4;  // up to 64 activation rows per pass
 
@@ -197,6 +180,9 @@ __global__ __launch_bounds__(256) void gather_kernel(
 
   while (true) {
     const int pos = sh.pos;
+    // Every wave has read pos before wave 0 overwrites it below, so all waves
+    // agree on the trip count (and on every barrier).
+    __syncthreads();
     if (pos >= hi) break;
     if (wave == 0) {
       int p = pos, cnt = 0;
@@ -241,6 +227,7 @@ __global__ __launch_bounds__(256) void gather_kernel(
       sh.yrow[i] = yp;
     }
     __syncthreads();
+    if (cnt == 0) continue;  // uniform: the scan reached hi without a match
     if (cnt <= 16) {
       skinny_tile<TT, BITS, 1>(we, se, be, n, k, gs_shift, n0, sh);
     } else if (cnt <= 32) {

@@ -10,12 +10,13 @@ import subprocess
 
 import numpy as np
 import pytest
-import torch
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
 
 def _bf16_torch(f32: np.ndarray) -> np.ndarray:
+    import torch
+
     return torch.from_numpy(np.ascontiguousarray(f32, np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
 
 
@@ -52,12 +53,29 @@ def test_f16_conversion_matches_numpy(oracle):
 def test_16bit_to_f32_exhaustive(oracle):
     allb = np.arange(65536, dtype=np.uint16)
     finite_bf = ((allb & 0x7F80) != 0x7F80)
+    import torch
+
     bf = np.array([oracle.c_bits_to_f32(int(b), "bf16") for b in allb[finite_bf]], np.float32)
     ref = torch.from_numpy(allb[finite_bf].view(np.int16)).view(torch.bfloat16).float().numpy()
     assert np.array_equal(bf.view(np.uint32), ref.view(np.uint32))
     finite_h = ((allb & 0x7C00) != 0x7C00)
     h = np.array([oracle.c_bits_to_f32(int(b), "f16") for b in allb[finite_h]], np.float32)
     assert np.array_equal(h.view(np.uint32), allb[finite_h].view(np.float16).astype(np.float32).view(np.uint32))
+
+
+def test_half_ulp_bounds_t_rounding(oracle):
+    """half_ulp (used by the tolerance check) is a tight bound on |RNE_T(v) - v|."""
+    rng = np.random.default_rng(8)
+    v = (rng.standard_normal(100_000) * np.exp2(rng.integers(-20, 20, 100_000))).astype(np.float32)
+    for dtype in ("bf16", "f16"):
+        vv = v[np.abs(v) < 6e4] if dtype == "f16" else v
+        r = oracle.bits_to_f32(oracle.f32_to_bits(vv, dtype), dtype).astype(np.float64)
+        e = np.abs(r - vv.astype(np.float64))
+        h = oracle.half_ulp(vv, dtype)
+        assert np.all(e <= h * (1 + 1e-12))
+        assert np.max(e / h) > 0.99
+    assert oracle.half_ulp(np.array([16.0, 15.99, -300.0]), "bf16").tolist() == [0.0625, 0.03125, 1.0]
+    assert oracle.half_ulp(np.array([1.0]), "f16")[0] == 2.0 ** -11
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
