@@ -234,6 +234,33 @@ __device__ __forceinline__ bool fast_ok(float s, float b) {
   return d0 <= span && d0 >= -span && d1 <= span && d1 >= -span;
 }
 
+// The same predicate on the raw 16-bit patterns of s and b (integer ops only).
+// bf16 (bias 127, 8-bit significand): d = e(b) - e(s) must lie in [-5, 21]
+// (|d-10| <= 15 and |d-6| <= 15) and |s| in [2^-100, 2^113].  f16 (bias 15,
+// 11-bit significand): d in [-2, 18]; every normal f16 is in range.
+template <typename TT>
+__device__ __forceinline__ bool fast_ok_bits(uint32_t sv, uint32_t bv);
+template <>
+__device__ __forceinline__ bool fast_ok_bits<BF16>(uint32_t sv, uint32_t bv) {
+  const int es = (int)((sv >> 7) & 0xffu), eb = (int)((bv >> 7) & 0xffu);
+  const bool sz = (sv & 0x7fffu) == 0u, bz = (bv & 0x7fffu) == 0u;
+  const bool b_norm = eb >= 27 && eb < 255;
+  if (sz) return bz || b_norm;
+  if (es < 27 || es > 240) return false;
+  const int d = eb - es;
+  return bz || (b_norm && d >= -5 && d <= 21);
+}
+template <>
+__device__ __forceinline__ bool fast_ok_bits<F16>(uint32_t sv, uint32_t bv) {
+  const int es = (int)((sv >> 10) & 0x1fu), eb = (int)((bv >> 10) & 0x1fu);
+  const bool sz = (sv & 0x7fffu) == 0u, bz = (bv & 0x7fffu) == 0u;
+  const bool b_norm = eb >= 1 && eb < 31;
+  if (sz) return bz || b_norm;
+  if (es < 1 || es > 30) return false;
+  const int d = eb - es;
+  return bz || (b_norm && d >= -2 && d <= 18);
+}
+
 // Natural 16-byte activation slice -> interleaved slot order of BITS.
 template <int BITS>
 __device__ __forceinline__ u32x4 interleave_x(u32x4 v) {

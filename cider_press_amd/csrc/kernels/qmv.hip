@@ -7,16 +7,20 @@
 // outputs the factored form exceeds the 2e-3 relative-L2 budget at K=4096.
 //
 // HBM-bound: algorithmic bytes per call = N*K*bits/8 + 2*N*(K/gs)*sizeof(T)
-// + (K + N)*sizeof(T).  The whole cost per weight is VALU dequantization, so
-// the dot products go to the matrix cores:
-//   - a workgroup owns 16 output rows and splits K over its WAVES waves;
-//   - the activation row is staged once into LDS, permuted into the
-//     interleaved slot order of the dequantizer (common.hpp), together with
-//     the 16 rows' (scale, bias) pairs and a workgroup-wide check that the
-//     single-FMA fast dequantization is exact for every group;
-//   - lane l streams row n0 + l%16, chunk 4u + l/16 (16 B of packed 4-bit
-//     weights: the 4 lane groups of a wave read 64 contiguous bytes of each
-//     of 16 rows), keeping PF chunks in flight per lane;
+// + (K + N)*sizeof(T).  Per weight the only real work is the VALU
+// dequantization, so the dot products go to the matrix cores:
+//   - a workgroup owns 16 output rows and gives each of its WAVES waves a
+//     contiguous quarter (eighth) of K;
+//   - loads are issued in the order they are needed: first the 16 rows'
+//     scales and biases and the activation (small), then the first PF weight
+//     chunks of every lane; the small loads return first, are staged into LDS
+//     (activation permuted into the dequantizer's interleaved slot order,
+//     per-group constants s, b, b-1024s, b-64s precomputed) and a workgroup
+//     vote picks the single-FMA fast dequantization when it is exact for
+//     every group, while the weight stream is already in flight;
+//   - lane l streams row n0 + l%16, chunk 4u + l/16 (16 B at 4-bit: each wave
+//     instruction reads 64 contiguous bytes of 16 rows, consecutive steps the
+//     next 64), PF chunks in flight;
 //   - each 8-element slice is dequantized into an MFMA B operand and issued
 //     as v_mfma_f32_16x16x32 against the activation slice broadcast to all 16
 //     A rows (the matrix cores are otherwise idle at M = 1);
@@ -29,114 +33,199 @@ namespace {
 
 using namespace dev;
 
-template <int BITS>
-struct QmvPrefetch {
-  static constexpr int PF = BITS <= 4 ? 8 : 4;  // chunks in flight per lane
+struct QmvGeom {
+  const uint32_t* wrow;
+  const uint16_t* xs;
+  const f32x4* gcrow;  // per-group (s, b, c0, c1) of this lane's row
+  int chunks, gs_shift, g;
+  int u0, u_end;       // this wave's unit range [u0, u_end)
 };
 
-template <typename TT, int BITS, int WAVES, bool FAST>
-__device__ __forceinline__ f32x4 qmv_stream(const uint32_t* __restrict__ wrow, bool row_ok,
-                                            const uint16_t* xs, const uint32_t* sbrow, int chunks,
-                                            int gs_shift, int wave, int g) {
-  constexpr int PF = QmvPrefetch<BITS>::PF;
-  const int units = (chunks + 3) >> 2;
-  const int nsteps = units > wave ? (units - wave + WAVES - 1) / WAVES : 0;
+// Chunk of step j (clamped to a valid chunk so loads never leave the row).
+template <bool EXACT>
+__device__ __forceinline__ int chunk_at(const QmvGeom& q, int j) {
+  const int c = 4 * (q.u0 + j) + q.g;
+  if constexpr (EXACT) return c;
+  return min(c, q.chunks - 1);
+}
+
+template <int BITS, bool EXACT>
+__device__ __forceinline__ void fetch(const QmvGeom& q, int j, uint32_t* dst) {
+  load_chunk<BITS>(q.wrow, (size_t)chunk_at<EXACT>(q, j), dst);
+}
+
+// One K step: 32 weights of this lane's row, 4 MFMAs.  In the inexact
+// geometry, steps past this wave's range use zero constants (exact zeros).
+template <typename TT, int BITS, bool EXACT, bool FAST>
+__device__ __forceinline__ void step(const QmvGeom& q, const uint32_t* cur, int j, f32x4& acc) {
+  const int c = chunk_at<EXACT>(q, j);
+  f32x4 gc = q.gcrow[(c << 5) >> q.gs_shift];
+  if constexpr (!EXACT) {
+    const bool live = q.u0 + j < q.u_end && 4 * (q.u0 + j) + q.g < q.chunks;
+    if (!live) gc = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const float s = gc[0], b = gc[1], c0 = gc[2], c1 = gc[3];
+  const float s16 = s * 0.0625f;
+  const u32x4* xa = reinterpret_cast<const u32x4*>(q.xs + c * 32);
+  acc = Mfma16<TT>::run(xa[0], dequant_slice<TT, BITS, FAST, 0>(cur, s, s16, b, c0, c1), acc);
+  acc = Mfma16<TT>::run(xa[1], dequant_slice<TT, BITS, FAST, 1>(cur, s, s16, b, c0, c1), acc);
+  acc = Mfma16<TT>::run(xa[2], dequant_slice<TT, BITS, FAST, 2>(cur, s, s16, b, c0, c1), acc);
+  acc = Mfma16<TT>::run(xa[3], dequant_slice<TT, BITS, FAST, 3>(cur, s, s16, b, c0, c1), acc);
+}
+
+// Steady state keeps PF loads in flight (loads unconditional, buffer index
+// static after unrolling), then drains the last PF steps.
+template <typename TT, int BITS, int PF, bool EXACT, bool FAST>
+__device__ __forceinline__ f32x4 stream(const QmvGeom& q, int nsteps, uint32_t (&buf)[PF][BITS]) {
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  uint32_t buf[PF][BITS];
-
-  auto chunk_of = [&](int j) { return 4 * (wave + WAVES * j) + g; };
-  auto fetch = [&](int j, uint32_t* dst) {
-    const int c = chunk_of(j);
-    if (row_ok && c < chunks) {
-      load_chunk<BITS>(wrow, (size_t)c, dst);
-    } else {
-#pragma unroll
-      for (int i = 0; i < BITS; ++i) dst[i] = 0u;
-    }
-  };
-
-#pragma unroll
-  for (int p = 0; p < PF; ++p)
-    if (p < nsteps) fetch(p, buf[p]);
-
-  for (int base = 0; base < nsteps; base += PF) {
+  for (int base = 0; base < nsteps - PF; base += PF) {
 #pragma unroll
     for (int p = 0; p < PF; ++p) {
-      const int j = base + p;
-      if (j < nsteps) {
-        uint32_t cur[BITS];
+      uint32_t cur[BITS];
 #pragma unroll
-        for (int i = 0; i < BITS; ++i) cur[i] = buf[p][i];
-        if (j + PF < nsteps) fetch(j + PF, buf[p]);
-        const int c = chunk_of(j);
-        const bool live = c < chunks;
-        const uint32_t sb = live ? sbrow[(c << 5) >> gs_shift] : 0u;
-        const float s = TT::to_f32((uint16_t)(sb & 0xffffu));
-        const float b = TT::to_f32((uint16_t)(sb >> 16));
-        const float s16 = s * 0.0625f;
-        const float c0 = FAST ? fmaf(-1024.f, s, b) : 0.f;
-        const float c1 = FAST ? fmaf(-64.f, s, b) : 0.f;
-        const u32x4* xa = reinterpret_cast<const u32x4*>(xs + (live ? c : 0) * 32);
-        const u32x4 zero = {0u, 0u, 0u, 0u};
-        acc = Mfma16<TT>::run(live ? xa[0] : zero, dequant_slice<TT, BITS, FAST, 0>(cur, s, s16, b, c0, c1), acc);
-        acc = Mfma16<TT>::run(live ? xa[1] : zero, dequant_slice<TT, BITS, FAST, 1>(cur, s, s16, b, c0, c1), acc);
-        acc = Mfma16<TT>::run(live ? xa[2] : zero, dequant_slice<TT, BITS, FAST, 2>(cur, s, s16, b, c0, c1), acc);
-        acc = Mfma16<TT>::run(live ? xa[3] : zero, dequant_slice<TT, BITS, FAST, 3>(cur, s, s16, b, c0, c1), acc);
-      }
+      for (int i = 0; i < BITS; ++i) cur[i] = buf[p][i];
+      fetch<BITS, EXACT>(q, base + PF + p, buf[p]);
+      step<TT, BITS, EXACT, FAST>(q, cur, base + p, acc);
     }
   }
+#pragma unroll
+  for (int p = 0; p < PF; ++p) step<TT, BITS, EXACT, FAST>(q, buf[p], nsteps - PF + p, acc);
   return acc;
 }
 
-template <typename TT, int BITS, int WAVES>
+constexpr int kSegSlots = 2;  // 16-B scale/bias segments held per thread before the weight loads
+constexpr int kXSlots = 4;    // 16-B activation slices held per thread before the weight loads
+
+template <typename TT>
+__device__ __forceinline__ f32x4 group_consts(uint32_t sv, uint32_t bv) {
+  const float s = TT::to_f32((uint16_t)sv), b = TT::to_f32((uint16_t)bv);
+  return f32x4{s, b, fmaf(-1024.f, s, b), fmaf(-64.f, s, b)};
+}
+
+template <typename TT, int BITS, int WAVES, int PF, bool EXACT>
 __global__ __launch_bounds__(64 * WAVES) void qmv_kernel(const uint32_t* __restrict__ w,
                                                          const uint16_t* __restrict__ scales,
                                                          const uint16_t* __restrict__ biases,
                                                          const uint16_t* __restrict__ x,
                                                          uint16_t* __restrict__ y, int n, int k,
                                                          int gs_shift) {
+  constexpr int NT = 64 * WAVES;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int G = k >> gs_shift;
-  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);                 // k elements, interleaved
-  uint32_t* sb = reinterpret_cast<uint32_t*>(smem + (size_t)k * 2);  // [16][G] (scale | bias << 16)
-  float* red = reinterpret_cast<float*>(smem + (size_t)k * 2 + (size_t)16 * G * 4);  // [WAVES][16]
+  const int GP = G + 1;  // padded row stride: the 16 rows of a lane group hit distinct banks
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);                          // k, interleaved
+  f32x4* gct = reinterpret_cast<f32x4*>(smem + (size_t)k * 2);                 // [16][GP]
+  float* red = reinterpret_cast<float*>(smem + (size_t)k * 2 + (size_t)16 * GP * 16);  // [WAVES][16]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int nl = lane & 15, g = lane >> 4;
+  const int nl = lane & 15;
   const int n0 = blockIdx.x * 16;
   const int row = n0 + nl;
-  const bool row_ok = row < n;
   const int chunks = k >> 5;
-  const size_t words_per_row = (size_t)k * BITS / 32;
-  const uint32_t* wrow = w + (size_t)(row_ok ? row : 0) * words_per_row;
+  const int units = (chunks + 3) >> 2;
+  const int per_wave = (units + WAVES - 1) / WAVES;
 
-  // Stage the activation (interleaved per 8-element slice).
-  for (int i = tid; i < (k >> 3); i += 64 * WAVES) {
+  QmvGeom q;
+  q.wrow = w + (size_t)(row < n ? row : 0) * ((size_t)k * BITS / 32);
+  q.xs = xs;
+  q.gcrow = gct + nl * GP;
+  q.chunks = chunks;
+  q.gs_shift = gs_shift;
+  q.g = lane >> 4;
+  q.u0 = wave * per_wave;
+  q.u_end = min(units, q.u0 + per_wave);
+  const int nsteps = (per_wave + PF - 1) / PF * PF;
+
+  // 1. Small loads first: (scale, bias) segments of the 16 rows, activation.
+  const bool vec = (G & 7) == 0 &&
+                   ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(biases)) & 15u) == 0;
+  const int segs = G >> 3;
+  u32x4 sv[kSegSlots], bv[kSegSlots];
+#pragma unroll
+  for (int t = 0; t < kSegSlots; ++t) {
+    const int i = tid + t * NT;
+    sv[t] = bv[t] = u32x4{0u, 0u, 0u, 0u};
+    if (vec && i < 16 * segs) {
+      const int r = i / segs, sg = i - r * segs;
+      if (n0 + r < n) {
+        sv[t] = *reinterpret_cast<const u32x4*>(scales + (size_t)(n0 + r) * G + sg * 8);
+        bv[t] = *reinterpret_cast<const u32x4*>(biases + (size_t)(n0 + r) * G + sg * 8);
+      }
+    }
+  }
+  u32x4 xv[kXSlots];
+#pragma unroll
+  for (int t = 0; t < kXSlots; ++t) {
+    const int i = tid + t * NT;
+    xv[t] = u32x4{0u, 0u, 0u, 0u};
+    if (i < (k >> 3)) xv[t] = *reinterpret_cast<const u32x4*>(x + (size_t)i * 8);
+  }
+
+  // 2. The weight stream.
+  uint32_t buf[PF][BITS];
+#pragma unroll
+  for (int p = 0; p < PF; ++p) fetch<BITS, EXACT>(q, p, buf[p]);
+
+  // 3. Stage to LDS (and anything beyond the register slots), vote.
+  bool ok = true;
+#pragma unroll
+  for (int t = 0; t < kXSlots; ++t) {
+    const int i = tid + t * NT;
+    if (i < (k >> 3)) *reinterpret_cast<u32x4*>(xs + (size_t)i * 8) = interleave_x<BITS>(xv[t]);
+  }
+  for (int i = tid + kXSlots * NT; i < (k >> 3); i += NT) {
     const u32x4 v = *reinterpret_cast<const u32x4*>(x + (size_t)i * 8);
     *reinterpret_cast<u32x4*>(xs + (size_t)i * 8) = interleave_x<BITS>(v);
   }
-  // Stage (scale, bias) of the 16 rows and decide the dequantization path.
-  bool ok = true;
-  for (int i = tid; i < 16 * G; i += 64 * WAVES) {
-    const int r = i / G, gi = i - r * G;
-    const int rr = n0 + r;
-    uint16_t sv = 0, bv = 0;
-    if (rr < n) {
-      sv = scales[(size_t)rr * G + gi];
-      bv = biases[(size_t)rr * G + gi];
+  if (vec) {
+#pragma unroll
+    for (int t = 0; t < kSegSlots; ++t) {
+      const int i = tid + t * NT;
+      if (i < 16 * segs) {
+        const int r = i / segs, sg = i - r * segs;
+        f32x4* dst = gct + r * GP + sg * 8;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const uint32_t s2 = sv[t][h], b2 = bv[t][h];
+          dst[2 * h] = group_consts<TT>(s2 & 0xffffu, b2 & 0xffffu);
+          dst[2 * h + 1] = group_consts<TT>(s2 >> 16, b2 >> 16);
+          ok = ok && fast_ok_bits<TT>(s2 & 0xffffu, b2 & 0xffffu) && fast_ok_bits<TT>(s2 >> 16, b2 >> 16);
+        }
+      }
     }
-    sb[i] = (uint32_t)sv | ((uint32_t)bv << 16);
-    ok = ok && fast_ok<TT>(TT::to_f32(sv), TT::to_f32(bv));
+    for (int i = tid + kSegSlots * NT; i < 16 * segs; i += NT) {
+      const int r = i / segs, sg = i - r * segs;
+      u32x4 s4 = {0u, 0u, 0u, 0u}, b4 = {0u, 0u, 0u, 0u};
+      if (n0 + r < n) {
+        s4 = *reinterpret_cast<const u32x4*>(scales + (size_t)(n0 + r) * G + sg * 8);
+        b4 = *reinterpret_cast<const u32x4*>(biases + (size_t)(n0 + r) * G + sg * 8);
+      }
+      f32x4* dst = gct + r * GP + sg * 8;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        dst[2 * h] = group_consts<TT>(s4[h] & 0xffffu, b4[h] & 0xffffu);
+        dst[2 * h + 1] = group_consts<TT>(s4[h] >> 16, b4[h] >> 16);
+        ok = ok && fast_ok_bits<TT>(s4[h] & 0xffffu, b4[h] & 0xffffu) && fast_ok_bits<TT>(s4[h] >> 16, b4[h] >> 16);
+      }
+    }
+  } else {
+    for (int i = tid; i < 16 * G; i += NT) {
+      const int r = i / G, gi = i - r * G;
+      uint32_t s1 = 0, b1 = 0;
+      if (n0 + r < n) {
+        s1 = scales[(size_t)(n0 + r) * G + gi];
+        b1 = biases[(size_t)(n0 + r) * G + gi];
+      }
+      gct[r * GP + gi] = group_consts<TT>(s1, b1);
+      ok = ok && fast_ok_bits<TT>(s1, b1);
+    }
   }
   const bool fast = __syncthreads_and(ok);
 
-  const uint32_t* sbrow = sb + nl * G;
-  f32x4 acc;
-  if (fast)
-    acc = qmv_stream<TT, BITS, WAVES, true>(wrow, row_ok, xs, sbrow, chunks, gs_shift, wave, g);
-  else
-    acc = qmv_stream<TT, BITS, WAVES, false>(wrow, row_ok, xs, sbrow, chunks, gs_shift, wave, g);
+  // 4. Stream the weights.
+  const f32x4 acc = fast ? stream<TT, BITS, PF, EXACT, true>(q, nsteps, buf)
+                         : stream<TT, BITS, PF, EXACT, false>(q, nsteps, buf);
 
   // D[m][n] sits in lane n + 16*(m/4), element m%4; every A row holds x, so
   // lanes 0..15 element 0 carry row n0 + lane.
@@ -156,25 +245,62 @@ int shift_of(int gs) {
   return s;
 }
 
-template <typename TT, int BITS, int WAVES>
-hipError_t launch_w(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k,
-                    size_t lds) {
-  hipLaunchKernelGGL((qmv_kernel<TT, BITS, WAVES>), dim3((unsigned)((n + 15) / 16)), dim3(64 * WAVES),
-                     lds, s, q.w, static_cast<const uint16_t*>(q.scales),
+template <typename TT, int BITS, int WAVES, int PF, bool EXACT>
+hipError_t launch_cfg(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k,
+                      size_t lds) {
+  if (lds > 64 * 1024) {
+    // Long rows need more than the default 64 KiB of dynamic LDS (gfx950 has
+    // 160 KiB per workgroup, shared with the kernel's static LDS); raise the
+    // kernel's limit once.
+    static const hipError_t attr = [] {
+      const void* fn = reinterpret_cast<const void*>(&qmv_kernel<TT, BITS, WAVES, PF, EXACT>);
+      hipFuncAttributes fa;
+      hipError_t e = hipFuncGetAttributes(&fa, fn);
+      if (e != hipSuccess) return e;
+      return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)(160 * 1024 - fa.sharedSizeBytes));
+    }();
+    if (attr != hipSuccess) return attr;
+    if (lds > 160 * 1024 - 1024) return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL((qmv_kernel<TT, BITS, WAVES, PF, EXACT>), dim3((unsigned)((n + 15) / 16)),
+                     dim3(64 * WAVES), lds, s, q.w, static_cast<const uint16_t*>(q.scales),
                      static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x),
                      static_cast<uint16_t*>(y), n, k, shift_of(q.gs));
   return hipGetLastError();
 }
 
+// EXACT geometry: every wave owns the same whole number of PF-step batches.
+template <typename TT, int BITS, int WAVES, int PF>
+hipError_t launch_pf(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k,
+                     size_t lds) {
+  const int chunks = k / 32;
+  const bool exact = chunks % 4 == 0 && (chunks / 4) % (WAVES * PF) == 0;
+  if (exact) return launch_cfg<TT, BITS, WAVES, PF, true>(s, q, x, y, n, k, lds);
+  return launch_cfg<TT, BITS, WAVES, PF, false>(s, q, x, y, n, k, lds);
+}
+
 template <typename TT, int BITS>
 hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k) {
   const size_t G = (size_t)k / q.gs;
-  const size_t lds = (size_t)k * 2 + 16 * G * 4 + 8 * 16 * 4;
-  if (lds > 64 * 1024)  // very long rows: the LDS-free small-M kernel
+  const size_t lds = (size_t)k * 2 + 16 * (G + 1) * 16 + 8 * 16 * 4;
+  if (lds > 160 * 1024)  // very long rows: the LDS-free small-M kernel
     return launch_qmm_skinny(s, q, x, y, 1, n, k);
-  // Few row blocks: split K over more waves to keep enough loads in flight.
-  if ((n + 15) / 16 >= 512) return launch_w<TT, BITS, 4>(s, q, x, y, n, k, lds);
-  return launch_w<TT, BITS, 8>(s, q, x, y, n, k, lds);
+  const int units = k / 128;
+  if constexpr (BITS == 4) {
+    // Few row blocks: split K over more waves to keep enough loads in flight.
+    if ((n + 15) / 16 >= 512) {
+      if (units % 32 == 0) return launch_pf<TT, BITS, 4, 8>(s, q, x, y, n, k, lds);
+      return launch_pf<TT, BITS, 4, 4>(s, q, x, y, n, k, lds);
+    }
+    if (units % 64 == 0) return launch_pf<TT, BITS, 8, 8>(s, q, x, y, n, k, lds);
+    return launch_pf<TT, BITS, 8, 4>(s, q, x, y, n, k, lds);
+  } else if constexpr (BITS == 8) {
+    if ((n + 15) / 16 >= 512) return launch_pf<TT, BITS, 4, 4>(s, q, x, y, n, k, lds);
+    return launch_pf<TT, BITS, 8, 4>(s, q, x, y, n, k, lds);
+  } else {
+    return launch_cfg<TT, BITS, 4, 4, false>(s, q, x, y, n, k, lds);
+  }
 }
 
 template <typename TT>
