@@ -324,6 +324,43 @@ __device__ __forceinline__ u32x4 dequant_slice(const uint32_t* w, float s, float
   }
 }
 
+// Natural-order fast dequantization of slice I (elements 8I..8I+7 in order,
+// pairs (e0,e1) (e2,e3) ...), for MFMA operands whose A side cannot be
+// permuted (activations streamed straight into LDS).  Per byte p: one
+// v_perm builds (b_p | 0x6400) in both halves, one AND keeps q_lo in the low
+// half and 16*q_hi in the high half: (1024 + q_{2p}, 1024 + 16 q_{2p+1}).
+template <typename TT, int BITS, bool FAST, int I>
+__device__ __forceinline__ u32x4 dequant_slice_nat(const uint32_t* w, float s, float s16, float b,
+                                                   float c0, float c1) {
+  if constexpr (BITS == 4 && FAST) {
+    const uint32_t M = 0x64646464u;
+    const uint32_t word = w[I];
+    u32x4 out;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t sel = 0x04000400u | (uint32_t)(p << 16) | (uint32_t)p;  // [b_p, 64, b_p, 64]
+      const uint32_t t = __builtin_amdgcn_perm(M, word, sel) & 0x64F0640Fu;
+      out[p] = TT::pack2(fmaf(s, f16lo(t), c0), fmaf(s16, f16hi(t), c1));
+    }
+    return out;
+  } else if constexpr (BITS == 8 && FAST) {
+    const uint32_t M = 0x64646464u;
+    const uint32_t w0 = w[2 * I], w1 = w[2 * I + 1];
+    const uint32_t p0 = __builtin_amdgcn_perm(M, w0, 0x04010400u);  // (1024+e0, 1024+e1)
+    const uint32_t p1 = __builtin_amdgcn_perm(M, w0, 0x04030402u);  // (1024+e2, 1024+e3)
+    const uint32_t p2 = __builtin_amdgcn_perm(M, w1, 0x04010400u);
+    const uint32_t p3 = __builtin_amdgcn_perm(M, w1, 0x04030402u);
+    return u32x4{TT::pack2(fmaf(s, f16lo(p0), c0), fmaf(s, f16hi(p0), c0)),
+                 TT::pack2(fmaf(s, f16lo(p1), c0), fmaf(s, f16hi(p1), c0)),
+                 TT::pack2(fmaf(s, f16lo(p2), c0), fmaf(s, f16hi(p2), c0)),
+                 TT::pack2(fmaf(s, f16lo(p3), c0), fmaf(s, f16hi(p3), c0))};
+  } else {
+    uint32_t o[4];
+    dequant8<TT, BITS, I>(w, s, s16, b, o);
+    return u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
 template <typename TT>
 struct Mfma16;
 template <>

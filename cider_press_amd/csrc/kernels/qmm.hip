@@ -185,6 +185,217 @@ __global__ __launch_bounds__(256) void qmm_kernel(const uint32_t* __restrict__ w
   }
 }
 
+// ---------------------------------------------------------------------------
+// Streaming prefill kernel (K % 128 == 0, 4/8-bit).
+//
+// Workgroup tile 128 (M) x 64 (N); its 4 waves are 2 N-halves x 2 K-halves,
+// each wave owning a 128 x 32 tile (four 32x32 accumulators).  The matrix
+// work per weight is then 128 MACs, enough to keep the VALU dequantization
+// (one W column dequantized exactly once per workgroup, by the wave that
+// owns it) below the MFMA time.  K advances in stages of 128: the K-half kh
+// of a wave takes k in [128s + 64kh, 128s + 64kh + 64).
+//   X: a ring of NSX LDS slots, each the 128 x 128 activation stage, filled by
+//      global_load_lds_dwordx4 (no VGPRs), rows of 256 B with 16-B columns
+//      XOR-swizzled by row (conflict-free ds_read_b128), NSX-1 stages ahead;
+//   W: each lane streams the 32-element chunk of its column for its K-half
+//      straight into registers, NSX-1 stages ahead, and dequantizes it into
+//      the four MFMA B operands of the stage;
+//   one s_barrier per stage; the two K-halves are summed through LDS at the
+//      end.  Workgroups are ordered so the M-tiles sharing a W slab land on
+//      the same XCD (same L2).
+// MFMA 32x32x16 k mapping: step t, lane group h = lane/32, element j <->
+// k = 128s + 64kh + 32h + 8t + j (the lane group's 32 k are one W chunk).
+// ---------------------------------------------------------------------------
+
+constexpr int SBM = 128, SBN = 64, SBK = 128;
+constexpr int NSX = 4;                           // LDS ring slots
+constexpr int SLOT_BYTES = SBM * SBK * 2;        // 32 KiB
+constexpr int AHEAD = NSX - 1;                   // stages issued ahead
+
+template <int BITS>
+struct StreamCfg {
+  static constexpr int WLOADS = BITS * 4 / 16;  // 16-B loads per chunk
+  static constexpr int VM = 8 + WLOADS + 2;      // VMEM instructions issued per stage
+};
+
+struct StreamGeom {
+  const uint32_t* wrow;
+  const uint16_t* srow;
+  const uint16_t* brow;
+  const uint16_t* xsrc[8];
+  int S, gs_shift, kh, hh, wave;
+};
+
+template <int BITS>
+__device__ __forceinline__ void stream_issue(const StreamGeom& g, unsigned char* smem, int s,
+                                             uint32_t* wdst, uint32_t& sb) {
+  const int sc = min(s, g.S - 1);  // tail stages re-load the last stage (never consumed)
+  unsigned char* slot = smem + (size_t)(s % NSX) * SLOT_BYTES;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    __builtin_amdgcn_global_load_lds(g.xsrc[j] + (size_t)sc * SBK, slot + (g.wave * 8 + j) * 1024, 16, 0, 0);
+  const int c = 4 * sc + 2 * g.kh + g.hh;
+  load_chunk<BITS>(g.wrow, (size_t)c, wdst);
+  const int gi = (c << 5) >> g.gs_shift;
+  sb = (uint32_t)g.srow[gi] | ((uint32_t)g.brow[gi] << 16);
+}
+
+template <typename TT, int BITS, bool FAST>
+__device__ __forceinline__ void stream_loop(const StreamGeom& g, unsigned char* smem,
+                                            uint32_t (&wbuf)[AHEAD][BITS], uint32_t (&sbuf)[AHEAD],
+                                            f32x16 (&acc)[4], int lane) {
+  const int l32 = lane & 31, csw = l32 & 15;
+  for (int s0 = 0; s0 < g.S; s0 += AHEAD) {
+#pragma unroll
+    for (int p = 0; p < AHEAD; ++p) {
+      const int s = s0 + p;
+      if (s < g.S) {  // uniform
+        // Stage s (X DMA, W chunk, scale/bias) is complete once only the
+        // loads of the AHEAD-1 later stages can still be in flight.
+        if constexpr (StreamCfg<BITS>::VM * (AHEAD - 1) == 22)
+          asm volatile("s_waitcnt vmcnt(22)" ::: "memory");
+        else
+          asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        uint32_t cur[BITS];
+#pragma unroll
+        for (int i = 0; i < BITS; ++i) cur[i] = wbuf[p][i];
+        const uint32_t sbv = sbuf[p];
+        stream_issue<BITS>(g, smem, s + AHEAD, wbuf[p], sbuf[p]);
+
+        const float sf = TT::to_f32((uint16_t)(sbv & 0xffffu));
+        const float bf = TT::to_f32((uint16_t)(sbv >> 16));
+        const float s16 = sf * 0.0625f;
+        const float c0 = FAST ? fmaf(-1024.f, sf, bf) : 0.f;
+        const float c1 = FAST ? fmaf(-64.f, sf, bf) : 0.f;
+        const unsigned char* slot = smem + (size_t)(s % NSX) * SLOT_BYTES;
+        u32x4 bop[4];
+        bop[0] = dequant_slice_nat<TT, BITS, FAST, 0>(cur, sf, s16, bf, c0, c1);
+        bop[1] = dequant_slice_nat<TT, BITS, FAST, 1>(cur, sf, s16, bf, c0, c1);
+        bop[2] = dequant_slice_nat<TT, BITS, FAST, 2>(cur, sf, s16, bf, c0, c1);
+        bop[3] = dequant_slice_nat<TT, BITS, FAST, 3>(cur, sf, s16, bf, c0, c1);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int colx = (8 * g.kh + 4 * g.hh + t) ^ csw;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const u32x4 a = *reinterpret_cast<const u32x4*>(slot + (32 * i + l32) * 256 + colx * 16);
+            acc[i] = Mfma32<TT>::run(a, bop[t], acc[i]);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <typename TT, int BITS>
+__global__ __launch_bounds__(256) void qmm_stream_kernel(const uint32_t* __restrict__ w,
+                                                         const uint16_t* __restrict__ scales,
+                                                         const uint16_t* __restrict__ biases,
+                                                         const uint16_t* __restrict__ x,
+                                                         uint16_t* __restrict__ y, int m, int n,
+                                                         int k, int gs_shift, int tiles_m,
+                                                         int tiles_n) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nh = wave & 1, kh = wave >> 1, hh = lane >> 5, l32 = lane & 31;
+
+  // XCD-aware tile order: consecutive linear ids (same XCD) walk M first.
+  const int nwg = tiles_m * tiles_n;
+  int lin = blockIdx.x;
+  if ((nwg & 7) == 0) lin = (lin & 7) * (nwg >> 3) + (lin >> 3);
+  const int mt = lin % tiles_m, nt = lin / tiles_m;
+  const int row0 = mt * SBM, col0 = nt * SBN;
+  const int G = k >> gs_shift;
+
+  // 1. Fast-path vote over the workgroup's 64 columns: loads first.
+  constexpr int VOTE_SLOTS = 8;
+  uint32_t vs[VOTE_SLOTS], vb[VOTE_SLOTS];
+  const int vcount = SBN * G;
+#pragma unroll
+  for (int t = 0; t < VOTE_SLOTS; ++t) {
+    const int i = tid + 256 * t;
+    vs[t] = vb[t] = 0u;
+    if (i < vcount) {
+      const int cc = min(col0 + i / G, n - 1);
+      const size_t off = (size_t)cc * G + (i % G);
+      vs[t] = scales[off];
+      vb[t] = biases[off];
+    }
+  }
+
+  // 2. Stream prologue.
+  StreamGeom g;
+  const int col = min(col0 + 32 * nh + l32, n - 1);
+  g.wrow = w + (size_t)col * ((size_t)k * BITS / 32);
+  g.srow = scales + (size_t)col * G;
+  g.brow = biases + (size_t)col * G;
+  g.S = k / SBK;
+  g.gs_shift = gs_shift;
+  g.kh = kh;
+  g.hh = hh;
+  g.wave = wave;
+  // X DMA: this wave fills blocks 8*wave .. 8*wave+7 (1 KiB = 4 rows each) of a
+  // slot; lane i of block b lands at row 4b + i/16, physical 16-B column i%16,
+  // which holds logical column (i%16) ^ (row%16).
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int rr = (wave * 8 + j) * 4 + (lane >> 4);
+    const int c = (lane & 15) ^ (rr & 15);
+    const int grow = min(row0 + rr, m - 1);
+    g.xsrc[j] = x + (size_t)grow * k + c * 8;
+  }
+  uint32_t wbuf[AHEAD][BITS];
+  uint32_t sbuf[AHEAD];
+#pragma unroll
+  for (int p = 0; p < AHEAD; ++p) stream_issue<BITS>(g, smem, p, wbuf[p], sbuf[p]);
+
+  // 3. Finish the vote (its loads are older than the stream's).
+  bool ok = true;
+#pragma unroll
+  for (int t = 0; t < VOTE_SLOTS; ++t) ok = ok && fast_ok_bits<TT>(vs[t], vb[t]);
+  for (int i = tid + 256 * VOTE_SLOTS; i < vcount; i += 256) {
+    const int cc = min(col0 + i / G, n - 1);
+    const size_t off = (size_t)cc * G + (i % G);
+    ok = ok && fast_ok_bits<TT>(scales[off], biases[off]);
+  }
+  const bool fast = __syncthreads_and(ok);
+
+  f32x16 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
+  if (fast)
+    stream_loop<TT, BITS, true>(g, smem, wbuf, sbuf, acc, lane);
+  else
+    stream_loop<TT, BITS, false>(g, smem, wbuf, sbuf, acc, lane);
+
+  // 4. Sum the two K-halves: kh = 1 waves park their tiles in LDS.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  float* park = reinterpret_cast<float*>(smem) + nh * (4 * 16 * 64);
+  if (kh == 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) park[(i * 16 + e) * 64 + lane] = acc[i][e];
+  }
+  __syncthreads();
+  if (kh == 0) {
+    const int gcol = col0 + 32 * nh + l32;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float v = acc[i][e] + park[(i * 16 + e) * 64 + lane];
+        const int grow = row0 + 32 * i + 8 * (e >> 2) + 4 * hh + (e & 3);
+        if (grow < m && gcol < n) y[(size_t)grow * n + gcol] = TT::from_f32(v);
+      }
+    }
+  }
+}
+
 int shift_of(int gs) {
   int s = 0;
   while ((1 << s) < gs) ++s;
@@ -203,7 +414,31 @@ hipError_t launch_cfg(hipStream_t s, const QuantArgs& q, const void* x, void* y,
 }
 
 template <typename TT, int BITS>
+hipError_t launch_stream(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n,
+                         int k) {
+  const size_t lds = (size_t)NSX * SLOT_BYTES;
+  static const hipError_t attr = [] {
+    const void* fn = reinterpret_cast<const void*>(&qmm_stream_kernel<TT, BITS>);
+    hipFuncAttributes fa;
+    hipError_t e = hipFuncGetAttributes(&fa, fn);
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)(160 * 1024 - fa.sharedSizeBytes));
+  }();
+  if (attr != hipSuccess) return attr;
+  const int tiles_m = (m + SBM - 1) / SBM, tiles_n = (n + SBN - 1) / SBN;
+  hipLaunchKernelGGL((qmm_stream_kernel<TT, BITS>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), lds,
+                     s, q.w, static_cast<const uint16_t*>(q.scales),
+                     static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x),
+                     static_cast<uint16_t*>(y), m, n, k, shift_of(q.gs), tiles_m, tiles_n);
+  return hipGetLastError();
+}
+
+template <typename TT, int BITS>
 hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k) {
+  if constexpr (BITS == 4 || BITS == 8) {
+    if (k % SBK == 0) return launch_stream<TT, BITS>(s, q, x, y, m, n, k);
+  }
   // Fill the chip: 128x128 tiles when they give at least ~2 workgroups per
   // CU, else 64-row tiles.
   const long tiles128 = (long)((m + 127) / 128) * ((n + 127) / 128);
