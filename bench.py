@@ -11,6 +11,17 @@ the launch stream.  The CPU baseline leg times the oracle's multithreaded
 dequantize-and-dot on the host.
 
     python bench.py [--steps K] [--warmup W] [--only qmv|qmm|all] [--no-cpu]
+
+HBM traffic (`roofline.traffic`) comes from rocprofv3 counter runs of this
+same script, calibrated against a plain device copy of known size:
+
+    rocprofv3 --pmc FETCH_SIZE -d D1 -o run --output-format csv -- python3 bench.py
+    rocprofv3 --pmc WRITE_SIZE -d D2 -o run --output-format csv -- python3 bench.py
+    rocprofv3 --pmc FETCH_SIZE -d D3 -o run --output-format csv -- python3 bench.py --only copy
+    rocprofv3 --pmc WRITE_SIZE -d D4 -o run --output-format csv -- python3 bench.py --only copy
+    python bench.py --pmc-summary D1 D2 D3 D4   # -> profiles/traffic.json
+
+`bench.py` reads profiles/traffic.json when it names the kernel being timed.
 """
 from __future__ import annotations
 
@@ -28,6 +39,13 @@ sys.path.insert(0, ROOT)
 METRIC = "qmv HBM GB/s (%peak) K4096×N12288 4b; qmm TFLOPS (%MFMA peak) M=512"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+
+
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic.json")
+COPY_BYTES = 512 << 20         # calibration copy: 512 MiB read + 512 MiB written
+QMV_KERNEL = "qmv_kernel<cpq::dev::BF16, 4"
+QMM_KERNEL = "qmm_stream_kernel<cpq::dev::BF16, 4>"
+COPY_KERNEL = "copy"
 
 
 def algo_bytes(m, n, k, gs, bits, tsize=2):
@@ -162,6 +180,78 @@ def cpu_baseline(q, budget_s):
                       f"over {budget_s:.0f} s, {threads} threads, oracle C dequantize-and-dot"}
 
 
+def bench_copy(args):
+    """Calibration leg: torch's device copy of COPY_BYTES, five times."""
+    import torch
+
+    src = torch.randint(0, 2**31 - 1, (COPY_BYTES // 4,), dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / 5
+    return {"calibration": "device copy", "bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES,
+            "ms": ms, "gbs": 2 * COPY_BYTES / (ms * 1e-3) / 1e9}
+
+
+def _pmc_per_dispatch(d, counter):
+    """Mean counter value (KiB) per dispatch, by kernel name, from rocprofv3 CSV output."""
+    import csv
+    import glob
+
+    acc = {}
+    for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                if r["Counter_Name"] != counter:
+                    continue
+                acc.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    return {k: (sum(v) / len(v), len(v)) for k, v in acc.items()}
+
+
+def pmc_summary(fetch_dir, write_dir, cfetch_dir, cwrite_dir):
+    """Scale FETCH_SIZE / WRITE_SIZE per dispatch by the copy calibration and
+    write profiles/traffic.json."""
+
+    def pick(tab, needle):
+        hits = [(k, v) for k, v in tab.items() if needle in k]
+        if not hits:
+            raise SystemExit(f"no dispatch of a kernel matching {needle!r}")
+        return max(hits, key=lambda kv: kv[1][1])
+
+    fetch, write = _pmc_per_dispatch(fetch_dir, "FETCH_SIZE"), _pmc_per_dispatch(write_dir, "WRITE_SIZE")
+    cfetch, cwrite = _pmc_per_dispatch(cfetch_dir, "FETCH_SIZE"), _pmc_per_dispatch(cwrite_dir, "WRITE_SIZE")
+    # The calibration copy is the kernel with the largest per-dispatch fetch.
+    ckey = max(cfetch, key=lambda k: cfetch[k][0])
+    kib = COPY_BYTES / 1024
+    f_fac = kib / cfetch[ckey][0]
+    w_fac = kib / cwrite[ckey][0]
+    out = {"copy_kernel": ckey, "copy_fetch_kib": cfetch[ckey][0], "copy_write_kib": cwrite[ckey][0],
+           "fetch_factor": f_fac, "write_factor": w_fac, "kernels": {}}
+    for tag, needle in (("qmv", QMV_KERNEL), ("qmm", QMM_KERNEL)):
+        name, (fk, nd) = pick(fetch, needle)
+        wk = pick(write, needle)[1][0]
+        out["kernels"][tag] = {"kernel": name, "dispatches": nd, "fetch_kib": fk, "write_kib": wk,
+                               "traffic_bytes": int(round((fk * f_fac + wk * w_fac) * 1024))}
+    os.makedirs(os.path.dirname(TRAFFIC_JSON), exist_ok=True)
+    with open(TRAFFIC_JSON, "w") as fh:
+        json.dump(out, fh, indent=1)
+    print(json.dumps(out, indent=1))
+
+
+def load_traffic(tag, needle):
+    try:
+        with open(TRAFFIC_JSON) as fh:
+            t = json.load(fh)["kernels"][tag]
+    except (OSError, KeyError, ValueError):
+        return None
+    return t["traffic_bytes"] if needle in t["kernel"] else None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -169,11 +259,16 @@ def main():
     ap.add_argument("--qmm-steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--copies", type=int, default=16)
-    ap.add_argument("--only", choices=["qmv", "qmm", "all"], default="all")
+    ap.add_argument("--only", choices=["qmv", "qmm", "all", "copy"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"))
     args = ap.parse_args()
+
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary)
+        return
 
     if args.gpus != 1:
         print(json.dumps({"error": f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported "
@@ -181,6 +276,10 @@ def main():
         sys.exit(2)
 
     from cider_press_amd.kernels import Device, KernelLibrary
+
+    if args.only == "copy":
+        print(json.dumps(bench_copy(args)), flush=True)
+        return
 
     dev = Device.system_default()
     lib = KernelLibrary.quantized(dev)
@@ -200,7 +299,8 @@ def main():
         line["value"] = round(q["gbs"], 2)
         line["ms_per_step"] = q["ms"]
         line["roofline"] = {"bound": "hbm", "achieved": round(q["gbs"], 2), "peak": HBM_PEAK_GBS,
-                            "unit": "GB/s", "frac": round(q["gbs"] / HBM_PEAK_GBS, 4), "traffic": None}
+                            "unit": "GB/s", "frac": round(q["gbs"] / HBM_PEAK_GBS, 4),
+                            "traffic": load_traffic("qmv", QMV_KERNEL)}
         line["parity"] = {"qmv": q["parity"]}
     if args.only in ("qmm", "all"):
         r = bench_qmm(dev, lib, args, rng)
@@ -209,7 +309,8 @@ def main():
                        "ms_per_step": r["ms"],
                        "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2),
                                     "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                    "frac": round(r["tflops"] / BF16_MFMA_PEAK_TFLOPS, 4), "traffic": None}}
+                                    "frac": round(r["tflops"] / BF16_MFMA_PEAK_TFLOPS, 4),
+                                    "traffic": load_traffic("qmm", QMM_KERNEL)}}
         line.setdefault("parity", {})["qmm"] = r["parity"]
         if args.only == "qmm":
             line["metric"] = METRIC

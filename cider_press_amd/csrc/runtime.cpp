@@ -64,7 +64,10 @@ cpq_status cpq_device_system_default(cpq_device** out) {
   d->ordinal = 0;
   d->cu_count = prop.multiProcessorCount;
   d->clock_khz = prop.clockRate;
-  std::snprintf(d->name, sizeof(d->name), "%s (%s)", prop.name, prop.gcnArchName);
+  if (prop.name[0])
+    std::snprintf(d->name, sizeof(d->name), "%s (%s)", prop.name, prop.gcnArchName);
+  else  // the marketing name is not always readable on shared boxes
+    std::snprintf(d->name, sizeof(d->name), "%s, %d CUs", prop.gcnArchName, prop.multiProcessorCount);
   *out = d;
   return CPQ_OK;
 }
