@@ -305,6 +305,12 @@ MUTATIONS = {
     "trunc": ("u += 0x7fffu + ((u >> 16) & 1u);", "u += 0u;"),
     # bias dropped from the dequantized weight
     "nobias": ("out[r * k + i] = from_f32(fmaf(s, (float)q[i], b), dtype);", "out[r * k + i] = from_f32(s * (float)q[i], dtype);"),
+    # wrong group index: element i reads the scale/bias of group (i+1)/gs
+    "groupidx": ("size_t g = r * groups_per_row + i / (size_t)gs;", "size_t g = r * groups_per_row + (i + 1) / (size_t)gs;"),
+    # last k term dropped from the reference matmul
+    "dropk": ("for (size_t kk = 0; kk < j->k; ++kk)", "for (size_t kk = 0; kk + 1 < j->k; ++kk)"),
+    # gather ignores the activation-row index
+    "lhs": ("size_t xr = lhs ? lhs[r] : r;", "size_t xr = r;"),
 }
 
 
@@ -325,26 +331,50 @@ def _build_mutant(tmp_path, name):
     return str(so)
 
 
-@pytest.mark.parametrize("name", sorted(MUTATIONS))
-def test_planted_mistake_is_caught(oracle, tmp_path, name):
-    import importlib
+def _pin_failures(mod, oracle):
+    """Every pin the planted-mistake test applies; True marks a failed pin."""
+    from cider_press_amd.synthetic import from_bits, make_weight, make_x
 
-    so = _build_mutant(tmp_path, name)
-    spec = importlib.util.spec_from_file_location("mutant_oracle", oracle.__file__)
-    mod = importlib.util.module_from_spec(spec)
-    spec.loader.exec_module(mod)
-    mod.LIB_PATH = so
-    mod._lib = None
     d = mod.read_safetensors(os.path.join(GOLDEN, "qmv.safetensors"))
     caught = []
     y = mod.qmv_mlx(d["x"].reshape(1, -1), d["w_q"], d["scales"], d["biases"], 1, 512, 512, 64, 4, "bf16")
     caught.append(not np.array_equal(mod.f32_to_bits(y, "bf16").reshape(-1), d["y_ref"]))
-    from cider_press_amd.synthetic import make_weight
-
     rng = np.random.default_rng(5)
     w_q, s, b = make_weight(rng, 8, 128, 64, 4, "bf16", bias_noise=1e-3)
     dq = mod.dequantize(w_q, s, b, 8, 128, 64, 4, "bf16")
     caught.append(not np.array_equal(dq, _independent_dequant(oracle.unpack(w_q, 128, 4), s, b, 64, "bf16")))
     fb = np.array([mod.c_f32_to_bits(float(v), "bf16") for v in _probe_floats(5000)], np.uint16)
     caught.append(not np.array_equal(fb, _bf16_torch(_probe_floats(5000))))
-    assert any(caught), f"mutation {name} slipped through every pin"
+    # reference matmul and gather against numpy float64 of independently dequantized W
+    x = make_x(rng, 5, 128, "bf16")
+    wd = from_bits(_independent_dequant(oracle.unpack(w_q, 128, 4), s, b, 64, "bf16"), "bf16").astype(np.float64)
+    xf = from_bits(x, "bf16").astype(np.float64)
+    caught.append(not np.allclose(mod.qmm_ref(x, w_q, s, b, 5, 8, 128, 64, 4, "bf16"), xf @ wd.T,
+                                  rtol=1e-12, atol=1e-10))
+    lhs = np.array([4, 0, 3, 1], np.uint32)
+    rhs = np.zeros(4, np.uint32)
+    yg = mod.gather_qmm_ref(x, lhs, rhs, w_q, s, b, 4, 8, 128, 64, 4, "bf16")
+    caught.append(not np.allclose(yg, xf[lhs] @ wd.T, rtol=1e-12, atol=1e-10))
+    return caught
+
+
+def _load_oracle_copy(oracle, so):
+    import importlib
+
+    spec = importlib.util.spec_from_file_location("mutant_oracle", oracle.__file__)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    if so is not None:
+        mod.LIB_PATH = so
+        mod._lib = None
+    return mod
+
+
+def test_pins_hold_for_unmutated_oracle(oracle):
+    assert not any(_pin_failures(_load_oracle_copy(oracle, None), oracle))
+
+
+@pytest.mark.parametrize("name", sorted(MUTATIONS))
+def test_planted_mistake_is_caught(oracle, tmp_path, name):
+    mod = _load_oracle_copy(oracle, _build_mutant(tmp_path, name))
+    assert any(_pin_failures(mod, oracle)), f"mutation {name} slipped through every pin"
