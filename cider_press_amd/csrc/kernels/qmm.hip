@@ -16,6 +16,8 @@
 // MFMA 32x32x16 operand layout: A[m][k] in lane m + 32*(k/8), element k%8;
 // B[k][n] in lane n + 32*(k/8), element k%8; D[m][n] in lane n + 32*((m/4)%2),
 // register 4*(m/8) + m%4.
+#include <algorithm>
+
 #include "../cpq_internal.hpp"
 #include "common.hpp"
 
@@ -396,6 +398,294 @@ __global__ __launch_bounds__(256) void qmm_stream_kernel(const uint32_t* __restr
   }
 }
 
+// ---------------------------------------------------------------------------
+// Staged prefill kernel (4/8-bit, K % 1024 == 0).
+//
+// Workgroup tile 128 (M) x 64 (N), K in stages of 128.  The activation stage
+// (128 rows x 128 k, 32 KiB) is copied into a ring of LDS slots with
+// buffer_load_dwordx4 ... lds, 3 stages ahead.  Each copy instruction moves
+// 4 rows x 256 contiguous bytes, so it needs 4 address translations; a
+// row-per-lane load in MFMA layout would need 16, and the L1 TLB serialises
+// translations (measured: it, not bandwidth, bounds such loads).  Rows keep
+// their 16-byte chunks XOR-swizzled by row, so the MFMA-layout ds_read_b128
+// is conflict-free.
+// Wave w owns the whole 128 x 64 tile for the k-slice [32w, 32w+32) of every
+// stage, so each staged activation byte is read from LDS exactly once and
+// each weight is dequantized once per workgroup:
+//   A: 8 x ds_read_b128 (row 16i + l%16, k 8(l/16)..+8 of the slice);
+//   W: 4 x (BITS/4) words per lane loaded straight into registers 7 stages
+//      ahead (lane l: word(s) l/16 of the slice's chunk of column 16j + l%16);
+//   32 v_mfma_f32_16x16x32 per stage, column block by column block, each
+//   block followed by the dequantization (natural k order) of that column's
+//   B operand for the next stage, which overlaps the next block's MFMAs.
+// One s_barrier per stage (the slot about to be refilled must have been read
+// by every wave); the 4 K-partial tiles are summed through LDS at the end.
+// MFMA 16x16x32 layout: A[m][k] lane m + 16(k/8), B[k][n] lane n + 16(k/8),
+// element k%8; D[m][n] lane n + 16(m/4), element m%4.
+// ---------------------------------------------------------------------------
+
+constexpr int QBM = 128, QBN = 64, QBK = 128;
+constexpr int QSLOT = QBM * QBK * 2;           // 32 KiB
+constexpr int QRW = 8;                         // weight register ring
+constexpr int QEPI = 132;                      // epilogue floats per lane (128 + pad)
+constexpr int QEPI_BYTES = 4 * 64 * QEPI * 4;  // 135168
+constexpr int QMAX_GROUPS = 256;               // groups per row the staged kernel accepts
+
+struct StageGeom {
+  __amdgpu_buffer_rsrc_t xr, wr;
+  uint32_t xoff[8];  // DMA source offset of this lane for copy block 8*wave + j (stage 0)
+  uint32_t woff[4];  // weight word offset (bytes) of column block j (stage 0)
+  uint32_t a_off;    // byte offset of this lane's A fragment (i = 0) within a slot
+  uint32_t c_off;    // byte offset of this lane's constants (group 0) in LDS
+  unsigned char* smem;
+  int wave, kw, gs_shift, S, nsx;
+};
+
+template <int BITS>
+__device__ __forceinline__ void stage_dma(const StageGeom& g, int s) {
+  unsigned char* slot = g.smem + (size_t)(s % g.nsx) * QSLOT;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        g.xr, (__attribute__((address_space(3))) void*)(slot + (g.wave * 8 + j) * 1024), 16, g.xoff[j],
+        s * (QBK * 2), 0, 0);
+}
+
+template <int BITS>
+__device__ __forceinline__ void stage_w(const StageGeom& g, int s, uint32_t (&wb)[4][BITS / 4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (BITS == 4) {
+      wb[j][0] = __builtin_amdgcn_raw_buffer_load_b32(g.wr, g.woff[j], s * 16 * BITS, 0);
+    } else {
+      const u32x2 t =
+          __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(g.wr, g.woff[j], s * 16 * BITS, 0));
+      wb[j][0] = t.x;
+      wb[j][1] = t.y;
+    }
+  }
+}
+
+// Raw constants of stage s: (s | b << 16) of the four column blocks.
+__device__ __forceinline__ u32x4 stage_consts(const StageGeom& g, int s) {
+  const int grp = (s * QBK + 32 * g.kw) >> g.gs_shift;
+  return *reinterpret_cast<const u32x4*>(g.smem + g.c_off + (size_t)grp * 256);
+}
+
+template <typename TT, int BITS, bool FAST>
+__device__ __forceinline__ u32x4 stage_dequant(const uint32_t (&wb)[BITS / 4], uint32_t sbv) {
+  const float sf = TT::to_f32((uint16_t)(sbv & 0xffffu)), bf = TT::to_f32((uint16_t)(sbv >> 16));
+  const float c0 = FAST ? fmaf(-1024.f, sf, bf) : 0.f;
+  const float c1 = FAST ? fmaf(-64.f, sf, bf) : 0.f;
+  return dequant_slice_nat<TT, BITS, FAST, 0>(wb, sf, sf * 0.0625f, bf, c0, c1);
+}
+
+// VMEM instructions issued after stage s's copies up to the start of stage s
+// -- the vmcnt that proves those copies complete.  Stage t issues 8 copies
+// (for t+3) when t+3 < S, then 4 weight loads (for t+7) when t+7 < S; the
+// prologue issues in the same pattern.  Only the last 8 stages (TAIL,
+// P = s - (S-8)) differ from the steady 4 + 12 + 12.
+template <bool TAIL, int P>
+constexpr int stage_vmcnt() {
+  if constexpr (!TAIL) {
+    return 28;
+  } else {
+    return 4 * (P <= 3) + 8 * (P <= 6) + 4 * (P <= 2) + 8 * (P <= 5) + 4 * (P <= 1);
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  // s_waitcnt simm16 (gfx9): vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] at [15:14].
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Stage s = s0 + P (s0 a multiple of 8: ring slots are static).
+template <typename TT, int BITS, bool FAST, bool TAIL, int P>
+__device__ __forceinline__ void stage_step(const StageGeom& g, int s, uint32_t (&wv)[QRW][4][BITS / 4],
+                                           u32x4 (&bop)[4], f32x4 (&acc)[8][4]) {
+  constexpr bool DMA = !TAIL || P + 3 < 8;
+  constexpr bool WLD = !TAIL || P + 7 < 8;
+  constexpr bool NEXT = !TAIL || P + 1 < 8;
+  wait_vmcnt<stage_vmcnt<TAIL, P>()>();
+  __builtin_amdgcn_s_barrier();
+  if constexpr (DMA) stage_dma<BITS>(g, s + 3);
+  if constexpr (WLD) stage_w<BITS>(g, s + 7, wv[(P + 7) % QRW]);
+  const unsigned char* slot = g.smem + (size_t)(s % g.nsx) * QSLOT + g.a_off;
+  u32x4 a[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const u32x4*>(slot + i * 4096);
+  u32x4 cn = {0u, 0u, 0u, 0u};
+  if constexpr (NEXT) cn = stage_consts(g, s + 1);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i][j] = Mfma16<TT>::run(a[i], bop[j], acc[i][j]);
+    if constexpr (NEXT) bop[j] = stage_dequant<TT, BITS, FAST>(wv[(P + 1) % QRW][j], cn[j]);
+  }
+}
+
+template <typename TT, int BITS, bool FAST, bool TAIL, int P = 0>
+__device__ __forceinline__ void stage_eight(const StageGeom& g, int s0, uint32_t (&wv)[QRW][4][BITS / 4],
+                                            u32x4 (&bop)[4], f32x4 (&acc)[8][4]) {
+  if constexpr (P < 8) {
+    stage_step<TT, BITS, FAST, TAIL, P>(g, s0 + P, wv, bop, acc);
+    stage_eight<TT, BITS, FAST, TAIL, P + 1>(g, s0, wv, bop, acc);
+  }
+}
+
+template <typename TT, int BITS, bool FAST>
+__device__ __forceinline__ void stage_loop(const StageGeom& g, uint32_t (&wv)[QRW][4][BITS / 4],
+                                           f32x4 (&acc)[8][4]) {
+  u32x4 bop[4];
+  const u32x4 c0 = stage_consts(g, 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) bop[j] = stage_dequant<TT, BITS, FAST>(wv[0][j], c0[j]);
+  int s0 = 0;
+  for (; s0 < g.S - 8; s0 += 8) stage_eight<TT, BITS, FAST, false>(g, s0, wv, bop, acc);
+  stage_eight<TT, BITS, FAST, true>(g, s0, wv, bop, acc);
+}
+
+template <typename TT, int BITS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void qmm_staged_kernel(
+    const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
+    const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+    int m, int n, int k, int gs_shift, int tiles_m, int tiles_n, int nsx, int sb_vec) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+
+  // Tile order: each XCD (linear ids congruent mod 8) gets a contiguous run
+  // of tiles, N fastest, so its workgroups share one activation panel in L2.
+  const int nwg = tiles_m * tiles_n;
+  int v = blockIdx.x;
+  if ((nwg & 7) == 0) v = (v & 7) * (nwg >> 3) + (v >> 3);
+  const int mt = v / tiles_n, nt = v % tiles_n;
+  const int row0 = mt * QBM, col0 = nt * QBN;
+  const int G = k >> gs_shift;
+
+  StageGeom g;
+  g.smem = smem;
+  g.wave = wave;
+  g.kw = wave;
+  g.gs_shift = gs_shift;
+  g.S = k / QBK;
+  g.nsx = nsx;
+  g.xr = __builtin_amdgcn_make_buffer_rsrc((void*)x, 0, (int)((uint32_t)m * (uint32_t)k * 2u), 0x00020000);
+  g.wr = __builtin_amdgcn_make_buffer_rsrc((void*)w, 0, (int)((uint32_t)n * (uint32_t)k / 8u * (uint32_t)BITS),
+                                           0x00020000);
+  // Copy block b = 8*wave + j holds rows 4b .. 4b+3; lane i lands at row
+  // 4b + i/16, physical chunk i%16, which holds logical chunk (i%16)^(row%16).
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int rr = (wave * 8 + j) * 4 + (lane >> 4);
+    const int c = (lane & 15) ^ (rr & 15);
+    const int grow = min(row0 + rr, m - 1);
+    g.xoff[j] = ((uint32_t)grow * (uint32_t)k + (uint32_t)(c * 8)) * 2u;
+  }
+  // A fragment of lane (m = l16, lg): row 16i + m, logical chunk 4*kw + lg.
+  g.a_off = (uint32_t)(l16 * 256 + (((4 * wave + lg) ^ l16) * 16));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int col = min(col0 + 16 * j + l16, n - 1);
+    g.woff[j] = (uint32_t)col * ((uint32_t)k / 8u * BITS) + (uint32_t)(wave * 4 * BITS) + (uint32_t)(lg * BITS);
+  }
+  const uint32_t cst_base = (uint32_t)nsx * QSLOT;
+  g.c_off = cst_base + (uint32_t)l16 * 16;
+
+  // 1. Prologue loads in the steady-state issue pattern: W for stages 0..3,
+  //    then (copies of stage t, W of stage t+4) for t = 0..2.
+  uint32_t wv[QRW][4][BITS / 4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) stage_w<BITS>(g, t, wv[t]);
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    stage_dma<BITS>(g, t);
+    stage_w<BITS>(g, t + 4, wv[t + 4]);
+  }
+
+  // 2. Raw per-(column, group) constants into LDS, [(g*16 + n)*4 + j] for
+  //    column col0 + 16j + n; the workgroup votes on the fast dequantization.
+  //    Vector path: thread (block u, column c = tid % 64) loads 8 groups of
+  //    its column per block, all blocks' loads in flight together.
+  uint32_t* cst = reinterpret_cast<uint32_t*>(smem + cst_base);
+  bool ok = true;
+  auto put = [&](int c, int gi, uint32_t sv, uint32_t bv) {
+    ok = ok && fast_ok_bits<TT>(sv, bv);
+    cst[(gi * 16 + (c & 15)) * 4 + (c >> 4)] = sv | (bv << 16);
+  };
+  if (sb_vec) {
+    constexpr int MAXB = QMAX_GROUPS / 8 / 4;  // 8-group blocks per thread
+    const int c = tid & 63, col = min(col0 + c, n - 1);
+    const int nblk = G >> 3;
+    u32x4 sv[MAXB], bv[MAXB];
+#pragma unroll
+    for (int u = 0; u < MAXB; ++u) {
+      const int gb = (tid >> 6) + 4 * u;
+      if (gb < nblk) {
+        sv[u] = *reinterpret_cast<const u32x4*>(scales + (size_t)col * G + gb * 8);
+        bv[u] = *reinterpret_cast<const u32x4*>(biases + (size_t)col * G + gb * 8);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < MAXB; ++u) {
+      const int gb = (tid >> 6) + 4 * u;
+      if (gb < nblk) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          put(c, gb * 8 + e, (e & 1) ? sv[u][e >> 1] >> 16 : sv[u][e >> 1] & 0xffffu,
+              (e & 1) ? bv[u][e >> 1] >> 16 : bv[u][e >> 1] & 0xffffu);
+      }
+    }
+  } else {
+    for (int it = tid; it < 64 * G; it += 256) {
+      const int c = it & 63, gi = it >> 6;
+      const size_t off = (size_t)min(col0 + c, n - 1) * G + gi;
+      put(c, gi, scales[off], biases[off]);
+    }
+  }
+  const bool fast = __syncthreads_and(ok);
+
+  // 3. Stream K.
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (fast)
+    stage_loop<TT, BITS, true>(g, wv, acc);
+  else
+    stage_loop<TT, BITS, false>(g, wv, acc);
+
+  // 4. Sum the four K-partial tiles: every wave parks its tile, then thread
+  //    (wave, lane) adds up accumulator tiles 8*wave .. 8*wave+7 of its lane.
+  __syncthreads();
+  float* ep = reinterpret_cast<float*>(smem);
+  {
+    float* mine = ep + (wave * 64 + lane) * QEPI;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<f32x4*>(mine + 4 * (i * 4 + j)) = acc[i][j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int t = 8 * wave + q, i = t >> 2, j = t & 3;
+    f32x4 sum = *reinterpret_cast<const f32x4*>(ep + lane * QEPI + 4 * t);
+#pragma unroll
+    for (int w2 = 1; w2 < 4; ++w2) sum += *reinterpret_cast<const f32x4*>(ep + (w2 * 64 + lane) * QEPI + 4 * t);
+    const int gcol = col0 + 16 * j + l16;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int grow = row0 + 16 * i + 4 * lg + e;
+      if (grow < m && gcol < n) y[(size_t)grow * n + gcol] = TT::from_f32(sum[e]);
+    }
+  }
+}
+
 int shift_of(int gs) {
   int s = 0;
   while ((1 << s) < gs) ++s;
@@ -434,9 +724,52 @@ hipError_t launch_stream(hipStream_t s, const QuantArgs& q, const void* x, void*
   return hipGetLastError();
 }
 
+// LDS ring depth of the staged kernel: 4 slots when the constants fit
+// beside them in 160 KiB, else 3; 0 if not even that fits.
+int staged_slots(int k, int gs) {
+  const int G = k / gs;
+  const int budget = 160 * 1024 - 256;  // minus __syncthreads_and's static LDS
+  if (4 * QSLOT + G * 256 <= budget) return 4;
+  if (3 * QSLOT + G * 256 <= budget) return 3;
+  return 0;
+}
+
+// The staged kernel addresses X and W with 32-bit byte offsets.
+bool staged_fits(int m, int n, int k, int gs, int bits) {
+  const uint64_t xb = (uint64_t)m * k * 2, wb = (uint64_t)n * k * bits / 8;
+  return k % 1024 == 0 && k / gs <= QMAX_GROUPS && staged_slots(k, gs) > 0 && xb < (1ull << 31) &&
+         wb < (1ull << 31);
+}
+
+template <typename TT, int BITS>
+hipError_t launch_staged(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n,
+                         int k) {
+  static const hipError_t attr = [] {
+    const void* fn = reinterpret_cast<const void*>(&qmm_staged_kernel<TT, BITS>);
+    hipFuncAttributes fa;
+    hipError_t e = hipFuncGetAttributes(&fa, fn);
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)(160 * 1024 - fa.sharedSizeBytes));
+  }();
+  if (attr != hipSuccess) return attr;
+  const int G = k / q.gs;
+  const int nsx = staged_slots(k, q.gs);
+  const size_t lds = std::max((size_t)nsx * QSLOT + (size_t)G * 256, (size_t)QEPI_BYTES);
+  const int sb_vec = (G % 8 == 0) && (reinterpret_cast<uintptr_t>(q.scales) % 16 == 0) &&
+                     (reinterpret_cast<uintptr_t>(q.biases) % 16 == 0);
+  const int tiles_m = (m + QBM - 1) / QBM, tiles_n = (n + QBN - 1) / QBN;
+  hipLaunchKernelGGL((qmm_staged_kernel<TT, BITS>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), lds,
+                     s, q.w, static_cast<const uint16_t*>(q.scales),
+                     static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x),
+                     static_cast<uint16_t*>(y), m, n, k, shift_of(q.gs), tiles_m, tiles_n, nsx, sb_vec);
+  return hipGetLastError();
+}
+
 template <typename TT, int BITS>
 hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k) {
   if constexpr (BITS == 4 || BITS == 8) {
+    if (staged_fits(m, n, k, q.gs, BITS)) return launch_staged<TT, BITS>(s, q, x, y, m, n, k);
     if (k % SBK == 0) return launch_stream<TT, BITS>(s, q, x, y, m, n, k);
   }
   // Fill the chip: 128x128 tiles when they give at least ~2 workgroups per
