@@ -427,28 +427,35 @@ __global__ __launch_bounds__(256) void qmm_stream_kernel(const uint32_t* __restr
 constexpr int QBM = 128, QBN = 64, QBK = 128;
 constexpr int QSLOT = QBM * QBK * 2;           // 32 KiB
 constexpr int QRW = 8;                         // weight register ring
-constexpr int QEPI = 132;                      // epilogue floats per lane (128 + pad)
-constexpr int QEPI_BYTES = 4 * 64 * QEPI * 4;  // 135168
 constexpr int QMAX_GROUPS = 256;               // groups per row the staged kernel accepts
+constexpr int QEPI_MAX = 4 * 2 * 64 * (64 + 4) * 4;  // largest epilogue (MH = 2): 139264 B
 
 struct StageGeom {
   __amdgpu_buffer_rsrc_t xr, wr;
-  uint32_t xoff[8];  // DMA source offset of this lane for copy block 8*wave + j (stage 0)
+  uint32_t xoff[8];  // DMA source offset of this lane for its copy block j (stage 0)
   uint32_t woff[4];  // weight word offset (bytes) of column block j (stage 0)
   uint32_t a_off;    // byte offset of this lane's A fragment (i = 0) within a slot
   uint32_t c_off;    // byte offset of this lane's constants (group 0) in LDS
   unsigned char* smem;
-  int wave, kw, gs_shift, S, nsx;
+  int wave, kw, gs_shift, S;
 };
 
-template <int BITS>
-__device__ __forceinline__ void stage_dma(const StageGeom& g, int s) {
-  unsigned char* slot = g.smem + (size_t)(s % g.nsx) * QSLOT;
+// Ring slot of stage s; s0 (the 8-stage block base) is a multiple of 8, so
+// for NSX dividing 8 the slot is static.
+template <int NSX, int P>
+__device__ __forceinline__ int stage_slot(int s) {
+  if constexpr (8 % NSX == 0) return P % NSX;
+  return s % NSX;
+}
+
+template <int BITS, int NSX, int MH>
+__device__ __forceinline__ void stage_dma(const StageGeom& g, int s, int slot_index) {
+  unsigned char* slot = g.smem + (size_t)slot_index * QSLOT;
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
+  for (int j = 0; j < 8 / MH; ++j)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        g.xr, (__attribute__((address_space(3))) void*)(slot + (g.wave * 8 + j) * 1024), 16, g.xoff[j],
-        s * (QBK * 2), 0, 0);
+        g.xr, (__attribute__((address_space(3))) void*)(slot + (g.wave * (8 / MH) + j) * 1024), 16,
+        g.xoff[j], s * (QBK * 2), 0, 0);
 }
 
 template <int BITS>
@@ -480,17 +487,17 @@ __device__ __forceinline__ u32x4 stage_dequant(const uint32_t (&wb)[BITS / 4], u
   return dequant_slice_nat<TT, BITS, FAST, 0>(wb, sf, sf * 0.0625f, bf, c0, c1);
 }
 
-// VMEM instructions issued after stage s's copies up to the start of stage s
-// -- the vmcnt that proves those copies complete.  Stage t issues 8 copies
+// VMEM instructions issued after stage s+1's copies up to the start of stage
+// s -- the vmcnt that proves those copies complete.  Stage t issues 8 copies
 // (for t+3) when t+3 < S, then 4 weight loads (for t+7) when t+7 < S; the
 // prologue issues in the same pattern.  Only the last 8 stages (TAIL,
-// P = s - (S-8)) differ from the steady 4 + 12 + 12.
-template <bool TAIL, int P>
+// P = s - (S-8)) differ from the steady 4 + 12.
+template <int MH, bool TAIL, int P>
 constexpr int stage_vmcnt() {
   if constexpr (!TAIL) {
-    return 28;
+    return 8 + 8 / MH;
   } else {
-    return 4 * (P <= 3) + 8 * (P <= 6) + 4 * (P <= 2) + 8 * (P <= 5) + 4 * (P <= 1);
+    return 4 * (P <= 2) + (8 / MH) * (P <= 5) + 4 * (P <= 1);
   }
 }
 
@@ -501,60 +508,81 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// Stage s = s0 + P (s0 a multiple of 8: ring slots are static).
-template <typename TT, int BITS, bool FAST, bool TAIL, int P>
+// Stage s = s0 + P.  On entry a[P & 1] holds stage s's A fragments and bop
+// its B operands.  The stage proves stage s+1's copies complete (own vmcnt,
+// then the barrier for the other waves'), refills the slot of stage s-1
+// (copies for s+3) and the weight ring (s+7), reads stage s+1's fragments
+// into a[(P + 1) & 1], and runs its MFMAs with the next stage's
+// dequantization between the column blocks.
+template <typename TT, int BITS, int NSX, int MH, bool FAST, bool TAIL, int P>
 __device__ __forceinline__ void stage_step(const StageGeom& g, int s, uint32_t (&wv)[QRW][4][BITS / 4],
-                                           u32x4 (&bop)[4], f32x4 (&acc)[8][4]) {
+                                           u32x4 (&a)[2][8 / MH], u32x4 (&bop)[4],
+                                           f32x4 (&acc)[8 / MH][4]) {
+  constexpr int NI = 8 / MH;
   constexpr bool DMA = !TAIL || P + 3 < 8;
   constexpr bool WLD = !TAIL || P + 7 < 8;
   constexpr bool NEXT = !TAIL || P + 1 < 8;
-  wait_vmcnt<stage_vmcnt<TAIL, P>()>();
-  __builtin_amdgcn_s_barrier();
-  if constexpr (DMA) stage_dma<BITS>(g, s + 3);
+  if constexpr (NEXT) {
+    wait_vmcnt<stage_vmcnt<MH, TAIL, P>()>();
+    __builtin_amdgcn_s_barrier();
+  }
+  if constexpr (DMA) stage_dma<BITS, NSX, MH>(g, s + 3, stage_slot<NSX, (P + 3) % 8>(s + 3));
   if constexpr (WLD) stage_w<BITS>(g, s + 7, wv[(P + 7) % QRW]);
-  const unsigned char* slot = g.smem + (size_t)(s % g.nsx) * QSLOT + g.a_off;
-  u32x4 a[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const u32x4*>(slot + i * 4096);
   u32x4 cn = {0u, 0u, 0u, 0u};
-  if constexpr (NEXT) cn = stage_consts(g, s + 1);
+  if constexpr (NEXT) {
+    const unsigned char* slot = g.smem + (size_t)stage_slot<NSX, (P + 1) % 8>(s + 1) * QSLOT + g.a_off;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) a[(P + 1) & 1][i] = *reinterpret_cast<const u32x4*>(slot + i * 4096);
+    cn = stage_consts(g, s + 1);
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i][j] = Mfma16<TT>::run(a[i], bop[j], acc[i][j]);
+    for (int i = 0; i < NI; ++i) acc[i][j] = Mfma16<TT>::run(a[P & 1][i], bop[j], acc[i][j]);
     if constexpr (NEXT) bop[j] = stage_dequant<TT, BITS, FAST>(wv[(P + 1) % QRW][j], cn[j]);
   }
 }
 
-template <typename TT, int BITS, bool FAST, bool TAIL, int P = 0>
+template <typename TT, int BITS, int NSX, int MH, bool FAST, bool TAIL, int P = 0>
 __device__ __forceinline__ void stage_eight(const StageGeom& g, int s0, uint32_t (&wv)[QRW][4][BITS / 4],
-                                            u32x4 (&bop)[4], f32x4 (&acc)[8][4]) {
+                                            u32x4 (&a)[2][8 / MH], u32x4 (&bop)[4],
+                                            f32x4 (&acc)[8 / MH][4]) {
   if constexpr (P < 8) {
-    stage_step<TT, BITS, FAST, TAIL, P>(g, s0 + P, wv, bop, acc);
-    stage_eight<TT, BITS, FAST, TAIL, P + 1>(g, s0, wv, bop, acc);
+    stage_step<TT, BITS, NSX, MH, FAST, TAIL, P>(g, s0 + P, wv, a, bop, acc);
+    stage_eight<TT, BITS, NSX, MH, FAST, TAIL, P + 1>(g, s0, wv, a, bop, acc);
   }
 }
 
-template <typename TT, int BITS, bool FAST>
+template <typename TT, int BITS, int NSX, int MH, bool FAST>
 __device__ __forceinline__ void stage_loop(const StageGeom& g, uint32_t (&wv)[QRW][4][BITS / 4],
-                                           f32x4 (&acc)[8][4]) {
-  u32x4 bop[4];
+                                           f32x4 (&acc)[8 / MH][4]) {
+  // Stage 0's copies are complete: the constant staging waited for every
+  // earlier load and the vote ended in a barrier.
+  u32x4 a[2][8 / MH], bop[4];
+  const unsigned char* slot = g.smem + g.a_off;
+#pragma unroll
+  for (int i = 0; i < 8 / MH; ++i) a[0][i] = *reinterpret_cast<const u32x4*>(slot + i * 4096);
   const u32x4 c0 = stage_consts(g, 0);
 #pragma unroll
   for (int j = 0; j < 4; ++j) bop[j] = stage_dequant<TT, BITS, FAST>(wv[0][j], c0[j]);
   int s0 = 0;
-  for (; s0 < g.S - 8; s0 += 8) stage_eight<TT, BITS, FAST, false>(g, s0, wv, bop, acc);
-  stage_eight<TT, BITS, FAST, true>(g, s0, wv, bop, acc);
+  for (; s0 < g.S - 8; s0 += 8) stage_eight<TT, BITS, NSX, MH, FAST, false>(g, s0, wv, a, bop, acc);
+  stage_eight<TT, BITS, NSX, MH, FAST, true>(g, s0, wv, a, bop, acc);
 }
 
-template <typename TT, int BITS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void qmm_staged_kernel(
+template <typename TT, int BITS, int NSX, int MH>
+__global__ __launch_bounds__(256 * MH) __attribute__((amdgpu_waves_per_eu(MH, MH))) void qmm_staged_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
-    int m, int n, int k, int gs_shift, int tiles_m, int tiles_n, int nsx, int sb_vec) {
+    int m, int n, int k, int gs_shift, int tiles_m, int tiles_n, int sb_vec) {
+  constexpr int NT = 256 * MH;   // threads
+  constexpr int NI = 8 / MH;     // 16-row blocks per wave
+  constexpr int RW = 128 / MH;   // rows per wave
+  constexpr int EPI = RW + 4;    // epilogue floats per lane (padded)
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kw = wave & 3, mh = wave >> 2;
   const int l16 = lane & 15, lg = lane >> 4;
 
   // Tile order: each XCD (linear ids congruent mod 8) gets a contiguous run
@@ -569,30 +597,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   StageGeom g;
   g.smem = smem;
   g.wave = wave;
-  g.kw = wave;
+  g.kw = kw;
   g.gs_shift = gs_shift;
   g.S = k / QBK;
-  g.nsx = nsx;
   g.xr = __builtin_amdgcn_make_buffer_rsrc((void*)x, 0, (int)((uint32_t)m * (uint32_t)k * 2u), 0x00020000);
   g.wr = __builtin_amdgcn_make_buffer_rsrc((void*)w, 0, (int)((uint32_t)n * (uint32_t)k / 8u * (uint32_t)BITS),
                                            0x00020000);
-  // Copy block b = 8*wave + j holds rows 4b .. 4b+3; lane i lands at row
+  // Copy block b = NI*wave + j holds rows 4b .. 4b+3; lane i lands at row
   // 4b + i/16, physical chunk i%16, which holds logical chunk (i%16)^(row%16).
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int rr = (wave * 8 + j) * 4 + (lane >> 4);
+  for (int j = 0; j < NI; ++j) {
+    const int rr = (wave * NI + j) * 4 + (lane >> 4);
     const int c = (lane & 15) ^ (rr & 15);
     const int grow = min(row0 + rr, m - 1);
     g.xoff[j] = ((uint32_t)grow * (uint32_t)k + (uint32_t)(c * 8)) * 2u;
   }
-  // A fragment of lane (m = l16, lg): row 16i + m, logical chunk 4*kw + lg.
-  g.a_off = (uint32_t)(l16 * 256 + (((4 * wave + lg) ^ l16) * 16));
+  // A fragment of lane (m = l16, lg): row RW*mh + 16i + m, logical chunk 4*kw + lg.
+  g.a_off = (uint32_t)((RW * mh + l16) * 256 + (((4 * kw + lg) ^ l16) * 16));
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int col = min(col0 + 16 * j + l16, n - 1);
-    g.woff[j] = (uint32_t)col * ((uint32_t)k / 8u * BITS) + (uint32_t)(wave * 4 * BITS) + (uint32_t)(lg * BITS);
+    g.woff[j] = (uint32_t)col * ((uint32_t)k / 8u * BITS) + (uint32_t)(kw * 4 * BITS) + (uint32_t)(lg * BITS);
   }
-  const uint32_t cst_base = (uint32_t)nsx * QSLOT;
+  const uint32_t cst_base = (uint32_t)NSX * QSLOT;
   g.c_off = cst_base + (uint32_t)l16 * 16;
 
   // 1. Prologue loads in the steady-state issue pattern: W for stages 0..3,
@@ -602,7 +629,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   for (int t = 0; t < 4; ++t) stage_w<BITS>(g, t, wv[t]);
 #pragma unroll
   for (int t = 0; t < 3; ++t) {
-    stage_dma<BITS>(g, t);
+    stage_dma<BITS, NSX, MH>(g, t, t);
     stage_w<BITS>(g, t + 4, wv[t + 4]);
   }
 
@@ -617,13 +644,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     cst[(gi * 16 + (c & 15)) * 4 + (c >> 4)] = sv | (bv << 16);
   };
   if (sb_vec) {
-    constexpr int MAXB = QMAX_GROUPS / 8 / 4;  // 8-group blocks per thread
+    constexpr int MAXB = QMAX_GROUPS / 8 / (NT / 64);  // 8-group blocks per thread
     const int c = tid & 63, col = min(col0 + c, n - 1);
     const int nblk = G >> 3;
     u32x4 sv[MAXB], bv[MAXB];
 #pragma unroll
     for (int u = 0; u < MAXB; ++u) {
-      const int gb = (tid >> 6) + 4 * u;
+      const int gb = (tid >> 6) + (NT / 64) * u;
       if (gb < nblk) {
         sv[u] = *reinterpret_cast<const u32x4*>(scales + (size_t)col * G + gb * 8);
         bv[u] = *reinterpret_cast<const u32x4*>(biases + (size_t)col * G + gb * 8);
@@ -631,7 +658,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 #pragma unroll
     for (int u = 0; u < MAXB; ++u) {
-      const int gb = (tid >> 6) + 4 * u;
+      const int gb = (tid >> 6) + (NT / 64) * u;
       if (gb < nblk) {
 #pragma unroll
         for (int e = 0; e < 8; ++e)
@@ -640,7 +667,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       }
     }
   } else {
-    for (int it = tid; it < 64 * G; it += 256) {
+    for (int it = tid; it < 64 * G; it += NT) {
       const int c = it & 63, gi = it >> 6;
       const size_t off = (size_t)min(col0 + c, n - 1) * G + gi;
       put(c, gi, scales[off], biases[off]);
@@ -649,38 +676,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const bool fast = __syncthreads_and(ok);
 
   // 3. Stream K.
-  f32x4 acc[8][4];
+  f32x4 acc[NI][4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < NI; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   if (fast)
-    stage_loop<TT, BITS, true>(g, wv, acc);
+    stage_loop<TT, BITS, NSX, MH, true>(g, wv, acc);
   else
-    stage_loop<TT, BITS, false>(g, wv, acc);
+    stage_loop<TT, BITS, NSX, MH, false>(g, wv, acc);
 
-  // 4. Sum the four K-partial tiles: every wave parks its tile, then thread
-  //    (wave, lane) adds up accumulator tiles 8*wave .. 8*wave+7 of its lane.
+  // 4. Sum the four K-partial tiles of each row half: every wave parks its
+  //    tile, then thread (kw, mh, lane) adds up accumulator tiles
+  //    NI*kw .. NI*kw+NI-1 of its lane over the four waves of its row half.
   __syncthreads();
   float* ep = reinterpret_cast<float*>(smem);
   {
-    float* mine = ep + (wave * 64 + lane) * QEPI;
+    float* mine = ep + (wave * 64 + lane) * EPI;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) *reinterpret_cast<f32x4*>(mine + 4 * (i * 4 + j)) = acc[i][j];
   }
   __syncthreads();
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int t = 8 * wave + q, i = t >> 2, j = t & 3;
-    f32x4 sum = *reinterpret_cast<const f32x4*>(ep + lane * QEPI + 4 * t);
+  for (int q = 0; q < NI; ++q) {
+    const int t = NI * kw + q, i = t >> 2, j = t & 3;
+    f32x4 sum = *reinterpret_cast<const f32x4*>(ep + ((4 * mh) * 64 + lane) * EPI + 4 * t);
 #pragma unroll
-    for (int w2 = 1; w2 < 4; ++w2) sum += *reinterpret_cast<const f32x4*>(ep + (w2 * 64 + lane) * QEPI + 4 * t);
+    for (int w2 = 1; w2 < 4; ++w2)
+      sum += *reinterpret_cast<const f32x4*>(ep + ((4 * mh + w2) * 64 + lane) * EPI + 4 * t);
     const int gcol = col0 + 16 * j + l16;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int grow = row0 + 16 * i + 4 * lg + e;
+      const int grow = row0 + RW * mh + 16 * i + 4 * lg + e;
       if (grow < m && gcol < n) y[(size_t)grow * n + gcol] = TT::from_f32(sum[e]);
     }
   }
@@ -741,11 +770,11 @@ bool staged_fits(int m, int n, int k, int gs, int bits) {
          wb < (1ull << 31);
 }
 
-template <typename TT, int BITS>
-hipError_t launch_staged(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n,
-                         int k) {
+template <typename TT, int BITS, int NSX, int MH>
+hipError_t launch_staged_n(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n,
+                           int k) {
   static const hipError_t attr = [] {
-    const void* fn = reinterpret_cast<const void*>(&qmm_staged_kernel<TT, BITS>);
+    const void* fn = reinterpret_cast<const void*>(&qmm_staged_kernel<TT, BITS, NSX, MH>);
     hipFuncAttributes fa;
     hipError_t e = hipFuncGetAttributes(&fa, fn);
     if (e != hipSuccess) return e;
@@ -754,16 +783,27 @@ hipError_t launch_staged(hipStream_t s, const QuantArgs& q, const void* x, void*
   }();
   if (attr != hipSuccess) return attr;
   const int G = k / q.gs;
-  const int nsx = staged_slots(k, q.gs);
-  const size_t lds = std::max((size_t)nsx * QSLOT + (size_t)G * 256, (size_t)QEPI_BYTES);
+  const size_t epi = (size_t)4 * MH * 64 * (128 / MH + 4) * 4;
+  const size_t lds = std::max((size_t)NSX * QSLOT + (size_t)G * 256, epi);
   const int sb_vec = (G % 8 == 0) && (reinterpret_cast<uintptr_t>(q.scales) % 16 == 0) &&
                      (reinterpret_cast<uintptr_t>(q.biases) % 16 == 0);
   const int tiles_m = (m + QBM - 1) / QBM, tiles_n = (n + QBN - 1) / QBN;
-  hipLaunchKernelGGL((qmm_staged_kernel<TT, BITS>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), lds,
-                     s, q.w, static_cast<const uint16_t*>(q.scales),
+  hipLaunchKernelGGL((qmm_staged_kernel<TT, BITS, NSX, MH>), dim3((unsigned)(tiles_m * tiles_n)),
+                     dim3(256 * MH), lds, s, q.w, static_cast<const uint16_t*>(q.scales),
                      static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x),
-                     static_cast<uint16_t*>(y), m, n, k, shift_of(q.gs), tiles_m, tiles_n, nsx, sb_vec);
+                     static_cast<uint16_t*>(y), m, n, k, shift_of(q.gs), tiles_m, tiles_n, sb_vec);
   return hipGetLastError();
+}
+
+#ifndef CPQ_STAGED_MH
+#define CPQ_STAGED_MH 1
+#endif
+
+template <typename TT, int BITS>
+hipError_t launch_staged(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n,
+                         int k) {
+  if (staged_slots(k, q.gs) == 4) return launch_staged_n<TT, BITS, 4, CPQ_STAGED_MH>(s, q, x, y, m, n, k);
+  return launch_staged_n<TT, BITS, 3, CPQ_STAGED_MH>(s, q, x, y, m, n, k);
 }
 
 template <typename TT, int BITS>
