@@ -159,6 +159,124 @@ def bench_qmm(dev, lib, args, rng):
             "parity": parity}
 
 
+def _weights(dev, rng, copies, n, k, gs, bits, dtype, bias_noise=0.0):
+    from cider_press_amd.synthetic import make_weight
+
+    out = []
+    for _ in range(copies):
+        w, s, b = make_weight(rng, n, k, gs, bits, dtype, bias_noise=bias_noise)
+        out.append((dev.upload(w.reshape(-1), "u32"), dev.upload(s.reshape(-1), dtype),
+                    dev.upload(b.reshape(-1), dtype)))
+    return out
+
+
+def _copies_for(nbytes, min_copies=2, working_set=600 << 20, cap=16):
+    """Enough rotated weight copies that the working set exceeds the 256 MB
+    Infinity Cache (bounded by `cap`)."""
+    return int(max(min_copies, min(cap, -(-working_set // max(nbytes, 1)))))
+
+
+def bench_configs(dev, lib, args, rng):
+    """The remaining configurations of the measurement table: cfg1, cfg2b
+    (decode), cfg3b/3c (prefill), cfg4 (small M through the routed op, all
+    three quantizations), cfg5 (routed experts).  Same timing method as the
+    headline: rotated weight copies, one graph replay between HIP events."""
+    from cider_press_amd.kernels import gather as kg
+    from cider_press_amd.kernels import qmm as kqmm
+    from cider_press_amd.kernels import qmv as kqmv
+    from cider_press_amd.synthetic import make_routing, make_x
+
+    steps = args.config_steps
+    res = {}
+
+    def qmv_case(name, n, k, dtype, bias_noise=0.0):
+        gs, bits = 64, 4
+        wb = n * k // 2 + 4 * n * (k // gs)
+        cps = _weights(dev, rng, _copies_for(wb), n, k, gs, bits, dtype, bias_noise)
+        X = dev.upload(make_x(rng, 1, k, dtype).reshape(-1), dtype)
+        Y = dev.alloc_buffer(n, dtype)
+        ms = time_graph(dev, steps, args.warmup,
+                        lambda c, i: kqmv.affine_qmv(c, lib, *cps[i % len(cps)], X, Y, k, gs, bits))
+        nb = algo_bytes(1, n, k, gs, bits)
+        res[name] = {"shape": f"x[1,{k}] . W[{n},{k}]^T 4b gs64 {dtype}", "us": round(ms * 1e3, 2),
+                     "GB/s": round(nb / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "copies": len(cps)}
+
+    def qmm_case(name, m, n, k):
+        gs, bits, dtype = 64, 4, "bf16"
+        wb = n * k // 2 + 4 * n * (k // gs)
+        cps = _weights(dev, rng, _copies_for(wb), n, k, gs, bits, dtype)
+        X = dev.upload(make_x(rng, m, k, dtype).reshape(-1), dtype)
+        Y = dev.alloc_buffer(m * n, dtype)
+        ms = time_graph(dev, max(10, steps // 4), args.warmup,
+                        lambda c, i: kqmm.affine_qmm_t(c, lib, *cps[i % len(cps)], X, Y, m, n, k, gs, bits))
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        res[name] = {"shape": f"X[{m},{k}] . W[{n},{k}]^T 4b gs64 bf16", "us": round(ms * 1e3, 2),
+                     "TFLOP/s": round(tf, 1), "mfma_frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 4), "copies": len(cps)}
+
+    qmv_case("cfg1", 2048, 2048, "f16", bias_noise=1e-3)
+    qmv_case("cfg2b", 4096, 12288, "bf16")
+    qmm_case("cfg3b", 512, 12288, 4096)
+    qmm_case("cfg3c_n4096", 2048, 4096, 4096)
+    qmm_case("cfg3c_n12288", 2048, 12288, 4096)
+
+    # cfg4: small M through the routed op (eval.rs routing), K = N = 4096.
+    rows = []
+    n = k = 4096
+    for bits, gs in ((4, 64), (4, 32), (8, 64)):
+        wb = n * k * bits // 8 + 4 * n * (k // gs)
+        cps = _weights(dev, rng, _copies_for(wb), n, k, gs, bits, "bf16")
+        for m in (1, 4, 16, 64):
+            X = dev.upload(make_x(rng, m, k, "bf16").reshape(-1), "bf16")
+            Y = dev.alloc_buffer(m * n, "bf16")
+            ms = time_graph(dev, steps, args.warmup,
+                            lambda c, i: kqmm.quantized_matmul(c, *cps[i % len(cps)], X, Y, m, n, k, gs, bits))
+            nb = algo_bytes(m, n, k, gs, bits)
+            tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+            rows.append({"bits": bits, "gs": gs, "m": m, "us": round(ms * 1e3, 2),
+                         "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                         "TFLOP/s": round(tf, 2), "mfma_frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 5),
+                         "kernel": "qmv" if m == 1 else ("small-M" if m <= 32 else "prefill")})
+        del cps
+    res["cfg4"] = rows
+
+    # cfg5: 128 experts, W_up [768, 2048] and W_down [2048, 768], 4b gs64;
+    # 256 tokens routed top-8 (uniform, without replacement) -> 2048 rows.
+    e, tokens, topk = 128, 256, 8
+    route = make_routing(rng, tokens, topk, e).reshape(-1)
+    lhs = np.repeat(np.arange(tokens, dtype=np.uint32), topk)
+    order = np.argsort(route, kind="stable")
+    for proj, (n, k) in (("up", (768, 2048)), ("down", (2048, 768))):
+        gs, bits = 64, 4
+        wb = e * (n * k // 2 + 4 * n * (k // gs))
+        cps = _weights(dev, rng, _copies_for(wb, cap=6), e * n, k, gs, bits, "bf16")
+        xin = make_x(rng, tokens if proj == "up" else tokens * topk, k, "bf16")
+        X = dev.upload(xin.reshape(-1), "bf16")
+        nrows = tokens * topk
+        Y = dev.alloc_buffer(nrows * n, "bf16")
+        for label, sorted_rows in (("unsorted", False), ("sorted", True)):
+            rhs = route[order] if sorted_rows else route
+            lh = lhs[order] if sorted_rows else lhs
+            if proj == "down":
+                lh = None  # row r of the down projection reads its own hidden row
+            R = dev.upload(rhs.astype(np.uint32), "u32")
+            L = dev.upload(lh.astype(np.uint32), "u32") if lh is not None else None
+            ms = time_graph(dev, max(10, steps // 2), args.warmup,
+                            lambda c, i: kg.affine_gather_qmm(c, lib, X, *cps[i % len(cps)], L, R, Y, nrows, n, k, e,
+                                                              gs, bits, sorted_indices=sorted_rows,
+                                                              x_rows=xin.shape[0]))
+            touched = len(np.unique(rhs))
+            nb = touched * (n * k // 2 + 4 * n * (k // gs)) + nrows * k * 2 + nrows * n * 2
+            tf = 2.0 * nrows * n * k / (ms * 1e-3) / 1e12
+            res[f"cfg5_{proj}_{label}"] = {
+                "shape": f"{nrows} rows x {e} experts W[{n},{k}] 4b gs64 bf16", "us": round(ms * 1e3, 2),
+                "GB/s": round(nb / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "TFLOP/s": round(tf, 2), "experts_touched": touched, "copies": len(cps)}
+        del cps
+    return res
+
+
 def cpu_baseline(q, budget_s):
     """Oracle dequantize-and-dot (T-rounded weights, fp32 accumulate) on the host."""
     from oracle import oracle as O
@@ -259,7 +377,9 @@ def main():
     ap.add_argument("--qmm-steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--copies", type=int, default=16)
-    ap.add_argument("--only", choices=["qmv", "qmm", "all", "copy"], default="all")
+    ap.add_argument("--only", choices=["qmv", "qmm", "all", "copy", "configs"], default="all")
+    ap.add_argument("--configs", action="store_true", help="also time cfg1/2b/3b/3c/4/5 (added to the line)")
+    ap.add_argument("--config-steps", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -319,6 +439,8 @@ def main():
             line["ms_per_step"] = r["ms"]
             line["steps"] = args.qmm_steps
             line["roofline"] = line["qmm"]["roofline"]
+    if args.configs or args.only == "configs":
+        line["configs"] = bench_configs(dev, lib, args, rng)
     if q is not None and not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(q, args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -76,6 +76,14 @@ hipError_t launch_qmm_skinny(hipStream_t s, const QuantArgs& q, const void* x, v
 hipError_t launch_qmm(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n,
                       int k);
 
+// Routed experts, expert-major kernel (4/8-bit, K % 128 == 0): one
+// workgroup per (expert, column chunk).  gather_expert_supported says whether
+// it applies; launch_gather_qmm uses it when it does.
+bool gather_expert_supported(int bits, int n_rows, int k);
+hipError_t launch_gather_expert(hipStream_t s, const QuantArgs& q, const void* x, int x_rows,
+                                const uint32_t* lhs, const uint32_t* rhs, int n_rows, void* y,
+                                int n_experts, int n, int k, bool sorted, int cu_count);
+
 // Routed experts.
 hipError_t launch_gather_qmm(hipStream_t s, const QuantArgs& q, const void* x, int x_rows,
                              const uint32_t* lhs, const uint32_t* rhs, int n_rows, void* y,

@@ -1,0 +1,399 @@
+// Routed-expert quantized matmul, expert-major, for gfx950:
+//   Y[r, :] = X[lhs[r], :] . dequant(W[rhs[r]])^T      (r < n_rows)
+//
+// Reference semantics: affine_gather_qmm_rhs / affine_gather_qmm_t
+// (kernels-mlx/.../quantized.h:2092-2172, 2242-2436): each routed row is
+// multiplied by its expert's weight, dequantized to T, fp32 accumulation.
+//
+// A workgroup (8 waves) owns one expert and one chunk of NC output columns.
+// Per pass it gathers up to R = 16*MB of the rows routed to its expert (in row
+// order: sorted routing by binary search, unsorted by per-64-row-block match
+// counts, their prefix, and a ballot placement), stages those rows'
+// activations in LDS once (16-byte chunks XOR-swizzled by row, conflict-free
+// for the MFMA reads), and then streams the chunk's weights:
+//   - wave w owns the 16-column slabs w, w+8, ... of the chunk; for each slab
+//     it walks K in steps of 4 chunks (lane l: column l%16, chunk 4u + l/16),
+//     8 steps of weights and their (scale, bias) in flight;
+//   - each step is dequantized in registers (natural k order; the exact
+//     single-FMA form when every lane's group allows it, else fmaf) into four
+//     v_mfma_f32_16x16x32 B operands and multiplied against the MB 16-row
+//     activation blocks read from LDS;
+//   - at a slab's last step the 16 x R tile is stored.
+// Weights stream from HBM exactly once per pass and activations are read
+// from L2 once per workgroup, so the kernel runs at the weight stream's rate
+// for routings with up to R rows per expert (more rows: more passes).
+#include <algorithm>
+
+#include "../cpq_internal.hpp"
+#include "common.hpp"
+
+namespace cpq {
+namespace {
+
+using namespace dev;
+
+constexpr int GX_WAVES = 8;
+constexpr int GX_THREADS = 64 * GX_WAVES;
+constexpr int GX_PF = 8;                   // steps in flight per wave
+constexpr int GX_XBYTES = 128 * 1024;      // LDS for the staged activation rows
+constexpr int GX_MAXBLK = 1024;            // 64-row routing blocks (n_rows <= 65536)
+
+struct GxShared {
+  int cnt[GX_MAXBLK];  // unsorted routing: matches of this expert per 64-row block, then prefix
+  int rows[64];        // routed rows of the pass (-1: none)
+  int xrow[64];        // their activation rows (-1: none / invalid)
+  int total, lo;
+};
+
+template <int BITS>
+struct GxStep {
+  uint32_t w[BITS];
+  uint32_t s, b;  // kept apart until used: combining them would wait for the loads
+};
+
+// Cursor over a wave's (slab, unit) steps: slab j of the wave is the 16-column
+// slab wave + 8j of the chunk, unit u its chunks 4u .. 4u+3 (lane group g
+// takes 4u + g).  Pointers advance incrementally (no per-step 64-bit math).
+template <int BITS>
+struct GxCursor {
+  const uint32_t* wrow;
+  const uint16_t* srow;
+  const uint16_t* brow;
+  int u, slab, col;
+  __device__ __forceinline__ void next(int units, int my_slabs, size_t wstride, size_t gstride, int n) {
+    if (++u == units) {
+      u = 0;
+      if (slab + 1 < my_slabs) {  // past the last slab: stay (clamped re-loads, never used)
+        ++slab;
+        col += 16 * GX_WAVES;
+        const bool ok = col < n;
+        wrow += ok ? wstride : 0;
+        srow += ok ? gstride : 0;
+        brow += ok ? gstride : 0;
+      }
+    }
+  }
+};
+
+template <typename TT, int BITS, int MB, bool FAST>
+__device__ __forceinline__ void gx_stream(GxCursor<BITS> ld, GxCursor<BITS> cp, int T, int units, int my_slabs,
+                                          size_t wstride, size_t gstride, int n, int chunks, int gs_shift,
+                                          int g, int nl, const unsigned char* xs, int k, const GxShared& sh,
+                                          uint16_t* __restrict__ y) {
+  auto load = [&](const GxCursor<BITS>& c, GxStep<BITS>& dst) {
+    const int ch = min(4 * c.u + g, chunks - 1);
+    load_chunk<BITS>(c.wrow, (size_t)ch, dst.w);
+    const int gi = (ch << 5) >> gs_shift;
+    dst.s = c.srow[gi];
+    dst.b = c.brow[gi];
+  };
+  GxStep<BITS> ring[GX_PF];
+#pragma unroll
+  for (int p = 0; p < GX_PF; ++p) {
+    load(ld, ring[p]);
+    ld.next(units, my_slabs, wstride, gstride, n);
+  }
+  const int TP = (T + GX_PF - 1) / GX_PF * GX_PF;
+  f32x4 acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t0 = 0; t0 < TP; t0 += GX_PF) {
+#pragma unroll
+    for (int p = 0; p < GX_PF; ++p) {
+      const int t = t0 + p;
+      const GxStep<BITS> cur = ring[p];
+      load(ld, ring[p]);  // clamped past the end: no branch, no wait
+      ld.next(units, my_slabs, wstride, gstride, n);
+      const int c = 4 * cp.u + g;
+      const bool live = t < T && c < chunks && cp.col < n;
+      const float sf = live ? TT::to_f32((uint16_t)cur.s) : 0.f;
+      const float bf = live ? TT::to_f32((uint16_t)cur.b) : 0.f;
+      const float s16 = sf * 0.0625f;
+      const float c0 = FAST ? fmaf(-1024.f, sf, bf) : 0.f, c1 = FAST ? fmaf(-64.f, sf, bf) : 0.f;
+      u32x4 bop[4];
+      bop[0] = dequant_slice<TT, BITS, FAST, 0>(cur.w, sf, s16, bf, c0, c1);
+      bop[1] = dequant_slice<TT, BITS, FAST, 1>(cur.w, sf, s16, bf, c0, c1);
+      bop[2] = dequant_slice<TT, BITS, FAST, 2>(cur.w, sf, s16, bf, c0, c1);
+      bop[3] = dequant_slice<TT, BITS, FAST, 3>(cur.w, sf, s16, bf, c0, c1);
+      const int cq = min(c, chunks - 1) * 4;  // first 16-byte chunk of this lane's 32 k
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const unsigned char* xr = xs + (size_t)(16 * mb + nl) * k * 2;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(xr + (size_t)(((cq + i) ^ nl) * 16));
+          acc[mb] = Mfma16<TT>::run(a, bop[i], acc[mb]);
+        }
+      }
+      if (cp.u == units - 1) {  // slab done (uniform)
+        if (t < T && cp.col < n) {
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int rl = 16 * mb + 4 * g + i;
+              const int r = sh.rows[rl];
+              if (r >= 0 && sh.xrow[rl] >= 0) y[(size_t)r * n + cp.col] = TT::from_f32(acc[mb][i]);
+            }
+          }
+        }
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      cp.next(units, my_slabs, wstride, gstride, n);
+    }
+  }
+}
+
+template <typename TT, int BITS, int MB>
+__global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
+    const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
+    const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, int x_rows,
+    const uint32_t* __restrict__ lhs, const uint32_t* __restrict__ rhs, int n_rows,
+    uint16_t* __restrict__ y, int n, int k, int gs_shift, int sorted, int nc, int sb_vec) {
+  constexpr int R = 16 * MB;
+  __shared__ GxShared sh;
+  extern __shared__ __attribute__((aligned(16))) unsigned char xs[];  // R x K activations
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nl = lane & 15, g = lane >> 4;
+  const uint32_t e = blockIdx.y;
+  const int c0 = blockIdx.x * nc;
+  const int ncols = min(nc, n - c0);
+  const int chunks = k >> 5;
+  const int units = (chunks + 3) >> 2;
+  const int G = k >> gs_shift;
+  const size_t words_per_row = (size_t)k * BITS / 32;
+  const uint32_t* we = w + (size_t)e * n * words_per_row;
+  const uint16_t* se = scales + (size_t)e * n * G;
+  const uint16_t* be = biases + (size_t)e * n * G;
+
+  // 1. Rows routed to e.
+  const int nblk = (n_rows + 63) >> 6;
+  if (sorted) {
+    if (tid == 0) {
+      int a = 0, b = n_rows;
+      while (a < b) { const int mid = (a + b) >> 1; if (rhs[mid] < e) a = mid + 1; else b = mid; }
+      const int lo = a;
+      b = n_rows;
+      while (a < b) { const int mid = (a + b) >> 1; if (rhs[mid] <= e) a = mid + 1; else b = mid; }
+      sh.lo = lo;
+      sh.total = a - lo;
+    }
+  } else {
+    for (int b = wave; b < nblk; b += GX_WAVES) {
+      const int r = (b << 6) + lane;
+      const unsigned long long mask = __ballot(r < n_rows && rhs[r] == e);
+      if (lane == 0) sh.cnt[b] = __popcll(mask);
+    }
+    __syncthreads();
+    if (tid == 0) {  // exclusive prefix over the blocks
+      int run = 0;
+      for (int b = 0; b < nblk; ++b) {
+        const int c = sh.cnt[b];
+        sh.cnt[b] = run;
+        run += c;
+      }
+      sh.total = run;
+      sh.lo = 0;
+    }
+  }
+  __syncthreads();
+  const int total = sh.total;
+  if (total == 0) return;  // uniform
+
+  // 2. Fast-path vote over the chunk's (column, group) pairs.
+  bool ok = true;
+  if (sb_vec) {
+    const int segs = G >> 3;
+    for (int i0 = tid; i0 < ncols * segs; i0 += 2 * GX_THREADS) {
+      u32x4 sv[2], bv[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int i = i0 + h * GX_THREADS;
+        sv[h] = bv[h] = u32x4{0u, 0u, 0u, 0u};
+        if (i < ncols * segs) {
+          const int c = i / segs, sg = i - c * segs;
+          sv[h] = *reinterpret_cast<const u32x4*>(se + (size_t)(c0 + c) * G + sg * 8);
+          bv[h] = *reinterpret_cast<const u32x4*>(be + (size_t)(c0 + c) * G + sg * 8);
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          ok = ok && fast_ok_bits<TT>(sv[h][q] & 0xffffu, bv[h][q] & 0xffffu) &&
+               fast_ok_bits<TT>(sv[h][q] >> 16, bv[h][q] >> 16);
+    }
+  } else {
+    for (int i = tid; i < ncols * G; i += GX_THREADS) {
+      const int c = i / G, gi = i - c * G;
+      ok = ok && fast_ok_bits<TT>(se[(size_t)(c0 + c) * G + gi], be[(size_t)(c0 + c) * G + gi]);
+    }
+  }
+  bool fast = __syncthreads_and(ok);
+  if constexpr (BITS != 4 && BITS != 8) fast = false;
+
+  // Wave w's slabs: 16-column slabs w, w+8, ... of the chunk.
+  const int nslab = (ncols + 15) >> 4;
+  const int my_slabs = nslab > wave ? (nslab - wave + GX_WAVES - 1) / GX_WAVES : 0;
+  const int T = my_slabs * units;  // live steps of this wave
+  const size_t wstride = (size_t)16 * GX_WAVES * words_per_row, gstride = (size_t)16 * GX_WAVES * G;
+  GxCursor<BITS> start;
+  start.u = 0;
+  start.slab = 0;
+  start.col = c0 + 16 * wave + nl;
+  const int col0 = min(start.col, n - 1);
+  start.wrow = we + (size_t)col0 * words_per_row;
+  start.srow = se + (size_t)col0 * G;
+  start.brow = be + (size_t)col0 * G;
+
+  for (int p0 = 0; p0 < total; p0 += R) {
+    // 3. The pass's rows and activation rows.
+    if (tid < R) sh.rows[tid] = -1;
+    __syncthreads();
+    if (sorted) {
+      if (tid < R && p0 + tid < total) sh.rows[tid] = sh.lo + p0 + tid;
+    } else {
+      for (int b = wave; b < nblk; b += GX_WAVES) {
+        const int base = sh.cnt[b];
+        const int next = b + 1 < nblk ? sh.cnt[b + 1] : total;
+        if (next <= p0 || base >= p0 + R) continue;  // uniform per wave
+        const int r = (b << 6) + lane;
+        const bool match = r < n_rows && rhs[r] == e;
+        const unsigned long long mask = __ballot(match);
+        const int rank = base + __popcll(mask & ((1ull << lane) - 1ull));
+        if (match && rank >= p0 && rank < p0 + R) sh.rows[rank - p0] = r;
+      }
+    }
+    __syncthreads();
+    if (tid < R) {
+      const int r = sh.rows[tid];
+      int xi = -1;
+      if (r >= 0) {
+        const uint32_t v = lhs ? lhs[r] : (uint32_t)r;
+        if (v < (uint32_t)x_rows) xi = (int)v;
+      }
+      sh.xrow[tid] = xi;
+    }
+    __syncthreads();
+
+    // 4. Activation rows into LDS in the dequantizer's slot order, 16-byte
+    //    chunk q of row i at i*K*2 + (q ^ (i & 15))*16.
+    const int kq = k >> 3;  // 16-byte chunks per row
+    for (int idx = tid; idx < R * kq; idx += GX_THREADS * 4) {
+      u32x4 v[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const int id = idx + h * GX_THREADS;
+        v[h] = u32x4{0u, 0u, 0u, 0u};
+        if (id < R * kq) {
+          const int i = id / kq, q = id - i * kq;
+          const int xi = sh.xrow[i];
+          if (xi >= 0) v[h] = *reinterpret_cast<const u32x4*>(x + (size_t)xi * k + (size_t)q * 8);
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const int id = idx + h * GX_THREADS;
+        if (id < R * kq) {
+          const int i = id / kq, q = id - i * kq;
+          *reinterpret_cast<u32x4*>(xs + (size_t)i * k * 2 + (size_t)((q ^ (i & 15)) * 16)) =
+              interleave_x<BITS>(v[h]);
+        }
+      }
+    }
+    __syncthreads();
+
+    // 5. Stream the weights of this wave's slabs.
+    if (T > 0) {
+      if (fast)
+        gx_stream<TT, BITS, MB, true>(start, start, T, units, my_slabs, wstride, gstride, n, chunks, gs_shift,
+                                      g, nl, xs, k, sh, y);
+      else
+        gx_stream<TT, BITS, MB, false>(start, start, T, units, my_slabs, wstride, gstride, n, chunks,
+                                       gs_shift, g, nl, xs, k, sh, y);
+    }
+    __syncthreads();  // LDS rows / activations are rewritten by the next pass
+  }
+}
+
+template <typename TT, int BITS, int MB>
+hipError_t launch_mb(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
+                     const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
+                     int gs_shift, int n_chunks, int nc) {
+  static const hipError_t attr = [] {
+    const void* fn = reinterpret_cast<const void*>(&gather_expert_kernel<TT, BITS, MB>);
+    hipFuncAttributes fa;
+    hipError_t e = hipFuncGetAttributes(&fa, fn);
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)(160 * 1024 - fa.sharedSizeBytes));
+  }();
+  if (attr != hipSuccess) return attr;
+  const size_t lds = (size_t)16 * MB * k * 2;
+  const int G = k / q.gs;
+  const int sb_vec = (G % 8 == 0) && (reinterpret_cast<uintptr_t>(q.scales) % 16 == 0) &&
+                     (reinterpret_cast<uintptr_t>(q.biases) % 16 == 0);
+  hipLaunchKernelGGL((gather_expert_kernel<TT, BITS, MB>), dim3((unsigned)n_chunks, (unsigned)n_experts),
+                     dim3(GX_THREADS), lds, s, q.w, static_cast<const uint16_t*>(q.scales),
+                     static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x), x_rows, lhs,
+                     rhs, n_rows, static_cast<uint16_t*>(y), n, k, gs_shift, (int)sorted, nc, sb_vec);
+  return hipGetLastError();
+}
+
+template <typename TT, int BITS>
+hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
+                    const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
+                    int cu_count) {
+  int gs_shift = 0;
+  while ((1 << gs_shift) < q.gs) ++gs_shift;
+  // Column chunks (whole multiples of 8 slabs = 128 columns): the count that
+  // minimises rounds-of-workgroups x work-per-workgroup over the CUs.
+  const int slabs128 = (n + 127) / 128;
+  int best = 1;
+  long best_cost = -1;
+  for (int c = 1; c <= slabs128; ++c) {
+    const long rounds = ((long)c * n_experts + cu_count - 1) / cu_count;
+    const long cost = rounds * ((slabs128 + c - 1) / c);
+    if (best_cost < 0 || cost < best_cost) {
+      best_cost = cost;
+      best = c;
+    }
+  }
+  const int nc = (slabs128 + best - 1) / best * 128;
+  const int n_chunks = (n + nc - 1) / nc;
+  if ((size_t)64 * k * 2 <= (size_t)GX_XBYTES)
+    return launch_mb<TT, BITS, 4>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, gs_shift,
+                                  n_chunks, nc);
+  if ((size_t)32 * k * 2 <= (size_t)GX_XBYTES)
+    return launch_mb<TT, BITS, 2>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, gs_shift,
+                                  n_chunks, nc);
+  return launch_mb<TT, BITS, 1>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, gs_shift,
+                                n_chunks, nc);
+}
+
+}  // namespace
+
+bool gather_expert_supported(int bits, int n_rows, int k) {
+  // k % 128: whole 16-chunk swizzle groups per staged row.
+  return (bits == 4 || bits == 8) && k % 128 == 0 && n_rows <= 64 * GX_MAXBLK &&
+         (size_t)16 * k * 2 <= (size_t)GX_XBYTES;
+}
+
+hipError_t launch_gather_expert(hipStream_t s, const QuantArgs& q, const void* x, int x_rows,
+                                const uint32_t* lhs, const uint32_t* rhs, int n_rows, void* y,
+                                int n_experts, int n, int k, bool sorted, int cu_count) {
+#define CPQ_GX(TT)                                                                                        \
+  switch (q.bits) {                                                                                       \
+    case 4: return launch_t<TT, 4>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, cu_count); \
+    case 8: return launch_t<TT, 8>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, cu_count); \
+    default: return hipErrorInvalidValue;                                                                 \
+  }
+  if (q.dtype == CPQ_DTYPE_BF16) { CPQ_GX(BF16) }
+  if (q.dtype == CPQ_DTYPE_F16) { CPQ_GX(F16) }
+#undef CPQ_GX
+  return hipErrorInvalidValue;
+}
+
+}  // namespace cpq

@@ -43,67 +43,202 @@ struct TileShared {
   int pos;
 };
 
-// One 16-column slab of W against up to 16*MB activation rows (pointers in sh).
-// All 256 threads must call it (contains __syncthreads).
+// Per-(column, group) constants (s, b, b - 1024 s, b - 64 s) of a 16-column
+// slab, gc[col * GP + g], and the workgroup's fast-path vote.  Split in two so
+// the caller can put the weight prefetch between the loads and their use:
+// slab_consts_load issues the loads (16-byte vectors of 8 groups when the
+// layout allows), slab_consts_store writes LDS, votes and ends in a barrier.
+constexpr int kConstSlots = 2;  // 16-byte segments per thread held in registers
+
+struct SlabConsts {
+  u32x4 sv[kConstSlots], bv[kConstSlots];
+};
+
+__device__ __forceinline__ void slab_consts_load(const uint16_t* __restrict__ scales,
+                                                 const uint16_t* __restrict__ biases, int n, int G,
+                                                 int n0, bool vec, SlabConsts& sc) {
+  const int segs = G >> 3;
+#pragma unroll
+  for (int t = 0; t < kConstSlots; ++t) {
+    sc.sv[t] = sc.bv[t] = u32x4{0u, 0u, 0u, 0u};
+    const int i = threadIdx.x + 256 * t;
+    if (vec && i < 16 * segs) {
+      const int c = i / segs, sg = i - c * segs;
+      if (n0 + c < n) {
+        sc.sv[t] = *reinterpret_cast<const u32x4*>(scales + (size_t)(n0 + c) * G + sg * 8);
+        sc.bv[t] = *reinterpret_cast<const u32x4*>(biases + (size_t)(n0 + c) * G + sg * 8);
+      }
+    }
+  }
+}
+
+template <typename TT>
+__device__ __forceinline__ bool slab_consts_store(const uint16_t* __restrict__ scales,
+                                                  const uint16_t* __restrict__ biases, int n, int G,
+                                                  int n0, bool vec, const SlabConsts& sc, f32x4* gc,
+                                                  int GP) {
+  bool ok = true;
+  auto put = [&](int c, int gi, uint32_t sv, uint32_t bv) {
+    ok = ok && fast_ok_bits<TT>(sv, bv);
+    const float sf = TT::to_f32((uint16_t)sv), bf = TT::to_f32((uint16_t)bv);
+    gc[c * GP + gi] = f32x4{sf, bf, fmaf(-1024.f, sf, bf), fmaf(-64.f, sf, bf)};
+  };
+  if (vec) {
+    const int segs = G >> 3;
+#pragma unroll
+    for (int t = 0; t < kConstSlots; ++t) {
+      const int i = threadIdx.x + 256 * t;
+      if (i < 16 * segs) {
+        const int c = i / segs, sg = i - c * segs;
+#pragma unroll
+        for (int h = 0; h < 8; ++h)
+          put(c, sg * 8 + h, (h & 1) ? sc.sv[t][h >> 1] >> 16 : sc.sv[t][h >> 1] & 0xffffu,
+              (h & 1) ? sc.bv[t][h >> 1] >> 16 : sc.bv[t][h >> 1] & 0xffffu);
+      }
+    }
+    for (int i = threadIdx.x + 256 * kConstSlots; i < 16 * segs; i += 256) {
+      const int c = i / segs, sg = i - c * segs;
+      u32x4 s4 = {0u, 0u, 0u, 0u}, b4 = {0u, 0u, 0u, 0u};
+      if (n0 + c < n) {
+        s4 = *reinterpret_cast<const u32x4*>(scales + (size_t)(n0 + c) * G + sg * 8);
+        b4 = *reinterpret_cast<const u32x4*>(biases + (size_t)(n0 + c) * G + sg * 8);
+      }
+#pragma unroll
+      for (int h = 0; h < 8; ++h)
+        put(c, sg * 8 + h, (h & 1) ? s4[h >> 1] >> 16 : s4[h >> 1] & 0xffffu,
+            (h & 1) ? b4[h >> 1] >> 16 : b4[h >> 1] & 0xffffu);
+    }
+  } else {
+    for (int it = threadIdx.x; it < 16 * G; it += 256) {
+      const int c = it / G, gi = it - c * G;
+      uint32_t sv = 0u, bv = 0u;
+      if (n0 + c < n) {
+        sv = scales[(size_t)(n0 + c) * G + gi];
+        bv = biases[(size_t)(n0 + c) * G + gi];
+      }
+      put(c, gi, sv, bv);
+    }
+  }
+  return __syncthreads_and(ok);
+}
+
+// One 16-column slab of W against up to 16*MB activation rows (pointers in
+// sh).  Each wave streams a contiguous quarter of K: PF weight chunks and the
+// next step's activation slices stay in flight while a step is dequantized
+// (natural k order) and multiplied.  Steps past the wave's range read clamped
+// addresses and use zero constants (exact zero weights).  The slab constants
+// are loaded first, the weight prefetch issued behind them, and only then
+// staged to LDS.  All 256 threads must call it (contains barriers).
+template <int BITS, int MB>
+struct SkinnyGeom {
+  const uint32_t* wrow;
+  const uint16_t* xr[MB];
+  const f32x4* gcol;
+  int u0, nu, nsteps, chunks, g, gs_shift;
+  bool col_ok;
+  __device__ __forceinline__ int chunk_of(int j) const { return min(4 * (u0 + j) + g, chunks - 1); }
+  __device__ __forceinline__ void load_x(int j, u32x4 (&dst)[MB][4]) const {
+    const int c = chunk_of(j);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[mb][i] = u32x4{0u, 0u, 0u, 0u};
+      if (xr[mb]) {
+        const u32x4* xs = reinterpret_cast<const u32x4*>(xr[mb] + (size_t)c * 32);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[mb][i] = xs[i];
+      }
+    }
+  }
+};
+
+template <typename TT, int BITS, int MB, bool FAST, int PF>
+__device__ __forceinline__ void skinny_stream(const SkinnyGeom<BITS, MB>& sg, uint32_t (&wbuf)[PF][BITS],
+                                              u32x4 (&xa)[2][MB][4], f32x4 (&acc)[MB]) {
+  for (int base = 0; base < sg.nsteps; base += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      const int j = base + p;
+      uint32_t cur[BITS];
+#pragma unroll
+      for (int i = 0; i < BITS; ++i) cur[i] = wbuf[p][i];
+      if (base + PF < sg.nsteps) load_chunk<BITS>(sg.wrow, (size_t)sg.chunk_of(j + PF), wbuf[p]);
+      if (j + 1 < sg.nsteps) sg.load_x(j + 1, xa[(p + 1) & 1]);
+      const int c = 4 * (sg.u0 + j) + sg.g;
+      f32x4 gcv = sg.gcol[(min(c, sg.chunks - 1) << 5) >> sg.gs_shift];
+      if (j >= sg.nu || c >= sg.chunks || !sg.col_ok) gcv = f32x4{0.f, 0.f, 0.f, 0.f};
+      const float sf = gcv[0], bf = gcv[1], s16 = sf * 0.0625f;
+      u32x4 bop[4];
+      bop[0] = dequant_slice_nat<TT, BITS, FAST, 0>(cur, sf, s16, bf, gcv[2], gcv[3]);
+      bop[1] = dequant_slice_nat<TT, BITS, FAST, 1>(cur, sf, s16, bf, gcv[2], gcv[3]);
+      bop[2] = dequant_slice_nat<TT, BITS, FAST, 2>(cur, sf, s16, bf, gcv[2], gcv[3]);
+      bop[3] = dequant_slice_nat<TT, BITS, FAST, 3>(cur, sf, s16, bf, gcv[2], gcv[3]);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[mb] = Mfma16<TT>::run(xa[p & 1][mb][i], bop[i], acc[mb]);
+    }
+  }
+}
+
 template <typename TT, int BITS, int MB>
 __device__ __forceinline__ void skinny_tile(const uint32_t* __restrict__ w,
                                             const uint16_t* __restrict__ scales,
                                             const uint16_t* __restrict__ biases, int n, int k,
-                                            int gs_shift, int n0, TileShared& sh) {
+                                            int gs_shift, int n0, f32x4* gc, TileShared& sh) {
+  constexpr int PF = 4;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nl = lane & 15;
-  const int g = lane >> 4;
   const int col = n0 + nl;
-  const bool col_ok = col < n;
-  const int chunks = k >> 5;
-  const int units = (chunks + 3) >> 2;
-  const size_t words_per_row = (size_t)k * BITS / 32;
-  const int groups_per_row = k >> gs_shift;
-  const uint32_t* wrow = w + (size_t)(col_ok ? col : 0) * words_per_row;
-  const uint16_t* srow = scales + (size_t)(col_ok ? col : 0) * groups_per_row;
-  const uint16_t* brow = biases + (size_t)(col_ok ? col : 0) * groups_per_row;
+  const int G = k >> gs_shift, GP = G + 1;
+  const bool vec = (G & 7) == 0 &&
+                   ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(biases)) & 15u) == 0;
 
-  const uint16_t* xr[MB];
+  SkinnyGeom<BITS, MB> sg;
+  sg.col_ok = col < n;
+  sg.chunks = k >> 5;
+  const int units = (sg.chunks + 3) >> 2;
+  const int per = (units + kWaves - 1) / kWaves;
+  sg.u0 = wave * per;
+  sg.nu = min(units, sg.u0 + per) - sg.u0;
+  sg.nsteps = (max(sg.nu, 0) + PF - 1) / PF * PF;
+  sg.g = lane >> 4;
+  sg.gs_shift = gs_shift;
+  sg.wrow = w + (size_t)(sg.col_ok ? col : 0) * ((size_t)k * BITS / 32);
+  sg.gcol = gc + nl * GP;
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) xr[mb] = sh.xrow[16 * mb + nl];
+  for (int mb = 0; mb < MB; ++mb) sg.xr[mb] = sh.xrow[16 * mb + nl];
 
+  // 1. Constants' loads, then the weight / activation prefetch behind them.
+  SlabConsts sc;
+  slab_consts_load(scales, biases, n, G, n0, vec, sc);
+  uint32_t wbuf[PF][BITS];
+  u32x4 xa[2][MB][4];
+  if (sg.nsteps > 0) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) load_chunk<BITS>(sg.wrow, (size_t)sg.chunk_of(p), wbuf[p]);
+    sg.load_x(0, xa[0]);
+  }
+  // 2. Constants into LDS, vote.
+  const bool fast = slab_consts_store<TT>(scales, biases, n, G, n0, vec, sc, gc, GP);
+
+  // 3. Stream.
   f32x4 acc[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  for (int u = wave; u < units; u += kWaves) {
-    const int c = 4 * u + g;
-    const bool live = c < chunks;
-    uint32_t wp[16];
-    if (live && col_ok) {
-      uint32_t wv[BITS];
-      load_chunk<BITS>(wrow, (size_t)c, wv);
-      const int gi = (c << 5) >> gs_shift;
-      dequant_chunk<TT, BITS>(wv, TT::to_f32(srow[gi]), TT::to_f32(brow[gi]), wp);
+  if (sg.nsteps > 0) {
+    if constexpr (BITS == 4 || BITS == 8) {
+      if (fast)
+        skinny_stream<TT, BITS, MB, true, PF>(sg, wbuf, xa, acc);
+      else
+        skinny_stream<TT, BITS, MB, false, PF>(sg, wbuf, xa, acc);
     } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) wp[i] = 0u;
-    }
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      u32x4 a[4];
-      if (live && xr[mb]) {
-        const u32x4* xs = reinterpret_cast<const u32x4*>(xr[mb] + (size_t)c * 32);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] = xs[i];
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] = u32x4{0u, 0u, 0u, 0u};
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        u32x4 b = {wp[4 * i], wp[4 * i + 1], wp[4 * i + 2], wp[4 * i + 3]};
-        acc[mb] = Mfma16<TT>::run(a[i], b, acc[mb]);
-      }
+      skinny_stream<TT, BITS, MB, false, PF>(sg, wbuf, xa, acc);
     }
   }
 
+  // 4. Sum the K-partial tiles.
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
@@ -116,9 +251,9 @@ __device__ __forceinline__ void skinny_tile(const uint32_t* __restrict__ w,
     for (int i = 0; i < 4; ++i) {
       float v = sh.red[0][mb][lane][i] + sh.red[1][mb][lane][i] + sh.red[2][mb][lane][i] +
                 sh.red[3][mb][lane][i];
-      const int m = 16 * mb + 4 * g + i;  // D row of element i in this lane
+      const int m = 16 * mb + 4 * sg.g + i;  // D row of element i in this lane
       uint16_t* yr = sh.yrow[m];
-      if (yr && col_ok) yr[col] = TT::from_f32(v);
+      if (yr && sg.col_ok) yr[col] = TT::from_f32(v);
     }
   }
   __syncthreads();
@@ -132,6 +267,8 @@ __global__ __launch_bounds__(256) void skinny_kernel(const uint32_t* __restrict_
                                                      uint16_t* __restrict__ y, int m, int n, int k,
                                                      int gs_shift) {
   __shared__ TileShared sh;
+  extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
+  f32x4* gc = reinterpret_cast<f32x4*>(dyn);
   const int n0 = blockIdx.x * 16;
   const int row0 = blockIdx.y * 16 * MB;
   if (threadIdx.x < 16 * MB) {
@@ -140,7 +277,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(const uint32_t* __restrict_
     sh.yrow[threadIdx.x] = r < m ? y + (size_t)r * n : nullptr;
   }
   __syncthreads();
-  skinny_tile<TT, BITS, MB>(w, scales, biases, n, k, gs_shift, n0, sh);
+  skinny_tile<TT, BITS, MB>(w, scales, biases, n, k, gs_shift, n0, gc, sh);
 }
 
 // Routed experts: workgroup (16-column slab, expert e).  Rows routed to e are
@@ -154,6 +291,8 @@ __global__ __launch_bounds__(256) void gather_kernel(
     const uint32_t* __restrict__ lhs, const uint32_t* __restrict__ rhs, int n_rows,
     uint16_t* __restrict__ y, int n, int k, int gs_shift, int sorted) {
   __shared__ TileShared sh;
+  extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
+  f32x4* gc = reinterpret_cast<f32x4*>(dyn);
   const int n0 = blockIdx.x * 16;
   const uint32_t e = blockIdx.y;
   const int lane = threadIdx.x & 63;
@@ -229,11 +368,11 @@ __global__ __launch_bounds__(256) void gather_kernel(
     __syncthreads();
     if (cnt == 0) continue;  // uniform: the scan reached hi without a match
     if (cnt <= 16) {
-      skinny_tile<TT, BITS, 1>(we, se, be, n, k, gs_shift, n0, sh);
+      skinny_tile<TT, BITS, 1>(we, se, be, n, k, gs_shift, n0, gc, sh);
     } else if (cnt <= 32) {
-      skinny_tile<TT, BITS, 2>(we, se, be, n, k, gs_shift, n0, sh);
+      skinny_tile<TT, BITS, 2>(we, se, be, n, k, gs_shift, n0, gc, sh);
     } else {
-      skinny_tile<TT, BITS, 4>(we, se, be, n, k, gs_shift, n0, sh);
+      skinny_tile<TT, BITS, 4>(we, se, be, n, k, gs_shift, n0, gc, sh);
     }
   }
 }
@@ -262,6 +401,9 @@ int shift_of(int gs) {
   return s;
 }
 
+// Dynamic LDS of the slab constants: 16 columns x (K/gs + 1) f32x4.
+size_t slab_consts_bytes(int k, int gs) { return (size_t)16 * (k / gs + 1) * 16; }
+
 template <typename TT, int BITS>
 hipError_t launch_skinny_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n,
                            int k) {
@@ -272,15 +414,16 @@ hipError_t launch_skinny_t(hipStream_t s, const QuantArgs& q, const void* x, voi
   const auto* xx = static_cast<const uint16_t*>(x);
   auto* yy = static_cast<uint16_t*>(y);
   const unsigned gx = (unsigned)((n + 15) / 16);
+  const size_t lds = slab_consts_bytes(k, q.gs);
   if (mb <= 1) {
-    hipLaunchKernelGGL((skinny_kernel<TT, BITS, 1>), dim3(gx, 1), dim3(256), 0, s, q.w, sc, bi, xx,
+    hipLaunchKernelGGL((skinny_kernel<TT, BITS, 1>), dim3(gx, 1), dim3(256), lds, s, q.w, sc, bi, xx,
                        yy, m, n, k, gs_shift);
   } else if (mb <= 2) {
-    hipLaunchKernelGGL((skinny_kernel<TT, BITS, 2>), dim3(gx, 1), dim3(256), 0, s, q.w, sc, bi, xx,
+    hipLaunchKernelGGL((skinny_kernel<TT, BITS, 2>), dim3(gx, 1), dim3(256), lds, s, q.w, sc, bi, xx,
                        yy, m, n, k, gs_shift);
   } else {
     const unsigned gy = (unsigned)((m + 63) / 64);
-    hipLaunchKernelGGL((skinny_kernel<TT, BITS, 4>), dim3(gx, gy), dim3(256), 0, s, q.w, sc, bi,
+    hipLaunchKernelGGL((skinny_kernel<TT, BITS, 4>), dim3(gx, gy), dim3(256), lds, s, q.w, sc, bi,
                        xx, yy, m, n, k, gs_shift);
   }
   return hipGetLastError();
@@ -297,8 +440,18 @@ hipError_t launch_gather_t(hipStream_t s, const QuantArgs& q, const void* x, int
                      status);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (gather_expert_supported(BITS, n_rows, k)) {
+    static const int cus = [] {
+      int dev = 0, cu = 0;
+      if (hipGetDevice(&dev) != hipSuccess ||
+          hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cu <= 0)
+        cu = 256;
+      return cu;
+    }();
+    return launch_gather_expert(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, cus);
+  }
   hipLaunchKernelGGL((gather_kernel<TT, BITS>), dim3((unsigned)((n + 15) / 16), (unsigned)n_experts),
-                     dim3(256), 0, s, q.w, static_cast<const uint16_t*>(q.scales),
+                     dim3(256), slab_consts_bytes(k, q.gs), s, q.w, static_cast<const uint16_t*>(q.scales),
                      static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x),
                      x_rows, lhs, rhs, n_rows, static_cast<uint16_t*>(y), n, k, gs_shift,
                      (int)sorted);
