@@ -10,7 +10,11 @@ steps are captured into a HIP graph and replayed, bracketed by HIP events on
 the launch stream.  The CPU baseline leg times the oracle's multithreaded
 dequantize-and-dot on the host.
 
-    python bench.py [--steps K] [--warmup W] [--only qmv|qmm|all] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--only qmv|qmm|all|configs] [--no-cpu] [--no-configs]
+
+The line's "configs" object times the other configurations of the
+measurement table (cfg1, cfg2b, cfg3b/3c, cfg4 small-M sweep through the
+routed op, cfg5 routed experts) the same way.
 
 HBM traffic (`roofline.traffic`) comes from rocprofv3 counter runs of this
 same script, calibrated against a plain device copy of known size:
@@ -44,7 +48,7 @@ BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic.json")
 COPY_BYTES = 512 << 20         # calibration copy: 512 MiB read + 512 MiB written
 QMV_KERNEL = "qmv_kernel<cpq::dev::BF16, 4"
-QMM_KERNEL = "qmm_stream_kernel<cpq::dev::BF16, 4>"
+QMM_KERNEL = "qmm_staged_kernel<cpq::dev::BF16, 4"
 COPY_KERNEL = "copy"
 
 
@@ -316,8 +320,16 @@ def bench_copy(args):
             "ms": ms, "gbs": 2 * COPY_BYTES / (ms * 1e-3) / 1e9}
 
 
+# Launch grids (threads) of the headline dispatches: qmv config 2a runs 768
+# workgroups of 256 threads, qmm config 3a 256 workgroups of 256 threads.  The
+# same kernels also serve the secondary configurations at other grids.
+QMV_GRID = 768 * 256
+QMM_GRID = 256 * 256
+
+
 def _pmc_per_dispatch(d, counter):
-    """Mean counter value (KiB) per dispatch, by kernel name, from rocprofv3 CSV output."""
+    """Mean counter value (KiB) per dispatch, by (kernel name, grid size),
+    from rocprofv3 CSV output."""
     import csv
     import glob
 
@@ -327,19 +339,40 @@ def _pmc_per_dispatch(d, counter):
             for r in csv.DictReader(fh):
                 if r["Counter_Name"] != counter:
                     continue
-                acc.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+                acc.setdefault((r["Kernel_Name"], int(r["Grid_Size"])), []).append(float(r["Counter_Value"]))
     return {k: (sum(v) / len(v), len(v)) for k, v in acc.items()}
+
+
+def trace_summary(d):
+    """Per (kernel, grid) durations from a rocprofv3 --kernel-trace run."""
+    import csv
+    import glob
+
+    acc = {}
+    for f in glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+                dur = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+                acc.setdefault((r["Kernel_Name"], grid), []).append(dur)
+    out = []
+    for (name, grid), v in sorted(acc.items(), key=lambda kv: -sum(kv[1])):
+        v.sort()
+        out.append({"kernel": name, "grid": grid, "calls": len(v), "avg_ns": sum(v) / len(v), "min_ns": v[0],
+                    "median_ns": v[len(v) // 2], "max_ns": v[-1]})
+    print(json.dumps(out, indent=1))
 
 
 def pmc_summary(fetch_dir, write_dir, cfetch_dir, cwrite_dir):
     """Scale FETCH_SIZE / WRITE_SIZE per dispatch by the copy calibration and
     write profiles/traffic.json."""
 
-    def pick(tab, needle):
-        hits = [(k, v) for k, v in tab.items() if needle in k]
+    def pick(tab, needle, grid):
+        hits = [(k, v) for k, v in tab.items() if needle in k[0] and k[1] == grid]
         if not hits:
-            raise SystemExit(f"no dispatch of a kernel matching {needle!r}")
-        return max(hits, key=lambda kv: kv[1][1])
+            raise SystemExit(f"no dispatch of a kernel matching {needle!r} at grid {grid}")
+        (name, _), val = max(hits, key=lambda kv: kv[1][1])
+        return name, val
 
     fetch, write = _pmc_per_dispatch(fetch_dir, "FETCH_SIZE"), _pmc_per_dispatch(write_dir, "WRITE_SIZE")
     cfetch, cwrite = _pmc_per_dispatch(cfetch_dir, "FETCH_SIZE"), _pmc_per_dispatch(cwrite_dir, "WRITE_SIZE")
@@ -348,12 +381,12 @@ def pmc_summary(fetch_dir, write_dir, cfetch_dir, cwrite_dir):
     kib = COPY_BYTES / 1024
     f_fac = kib / cfetch[ckey][0]
     w_fac = kib / cwrite[ckey][0]
-    out = {"copy_kernel": ckey, "copy_fetch_kib": cfetch[ckey][0], "copy_write_kib": cwrite[ckey][0],
+    out = {"copy_kernel": ckey[0], "copy_fetch_kib": cfetch[ckey][0], "copy_write_kib": cwrite[ckey][0],
            "fetch_factor": f_fac, "write_factor": w_fac, "kernels": {}}
-    for tag, needle in (("qmv", QMV_KERNEL), ("qmm", QMM_KERNEL)):
-        name, (fk, nd) = pick(fetch, needle)
-        wk = pick(write, needle)[1][0]
-        out["kernels"][tag] = {"kernel": name, "dispatches": nd, "fetch_kib": fk, "write_kib": wk,
+    for tag, needle, grid in (("qmv", QMV_KERNEL, QMV_GRID), ("qmm", QMM_KERNEL, QMM_GRID)):
+        name, (fk, nd) = pick(fetch, needle, grid)
+        wk = pick(write, needle, grid)[1][0]
+        out["kernels"][tag] = {"kernel": name, "grid": grid, "dispatches": nd, "fetch_kib": fk, "write_kib": wk,
                                "traffic_bytes": int(round((fk * f_fac + wk * w_fac) * 1024))}
     os.makedirs(os.path.dirname(TRAFFIC_JSON), exist_ok=True)
     with open(TRAFFIC_JSON, "w") as fh:
@@ -378,13 +411,18 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--copies", type=int, default=16)
     ap.add_argument("--only", choices=["qmv", "qmm", "all", "copy", "configs"], default="all")
-    ap.add_argument("--configs", action="store_true", help="also time cfg1/2b/3b/3c/4/5 (added to the line)")
+    ap.add_argument("--no-configs", action="store_true", help="skip the cfg1/2b/3b/3c/4/5 table")
     ap.add_argument("--config-steps", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"))
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_DIR")
     args = ap.parse_args()
+
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
+        return
 
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
@@ -439,7 +477,7 @@ def main():
             line["ms_per_step"] = r["ms"]
             line["steps"] = args.qmm_steps
             line["roofline"] = line["qmm"]["roofline"]
-    if args.configs or args.only == "configs":
+    if (args.only == "all" and not args.no_configs) or args.only == "configs":
         line["configs"] = bench_configs(dev, lib, args, rng)
     if q is not None and not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(q, args.cpu_seconds)
