@@ -217,6 +217,9 @@ def test_qmv_capacity_rejected_before_launch(device, library):
     (33, 96, 256, 64, 2, "bf16"),
     (40, 64, 384, 32, 6, "bf16"),
     (2, 32, 128, 64, 4, "bf16"),
+    (96, 160, 4096, 32, 4, "f16"),         # staged kernel: 3-slot ring (128 groups), N and M tails
+    (136, 224, 2048, 64, 8, "f16"),        # staged kernel, 8-bit, f16
+    (256, 128, 12288, 128, 4, "bf16"),     # staged kernel, long K
 ])
 def test_qmm_t_parity(device, library, oracle, m, n, k, gs, bits, dtype):
     rng = np.random.default_rng(m * 7 + n + bits)
@@ -313,6 +316,21 @@ def test_gather_identity_lhs_and_skewed_routing(device, library, oracle):
     y = run_gather(device, library, x, w_q, s, b, None, rhs, rows, n, k, e, gs, 8, "bf16", False)
     ref = oracle.gather_qmm_ref(x, None, rhs, w_q, s, b, rows, n, k, gs, 8, "bf16")
     assert_tol(oracle, y, ref, x, k, "bf16", "gather skewed")
+
+
+@pytest.mark.parametrize("bits,k,dtype", [(4, 1024, "f16"), (8, 2048, "bf16"), (4, 4096, "bf16")])
+def test_gather_expert_kernel_passes(device, library, oracle, bits, k, dtype):
+    """Expert-major kernel: experts with 0, a few, and more rows than one pass holds
+    (16 * MB rows, MB = 4 / 2 / 1 at K = 1024 / 2048 / 4096), unsorted routing."""
+    rng = np.random.default_rng(31 + bits + k)
+    e, n, gs, rows = 5, 272, 64, 150
+    w_q, s, b = _experts(rng, e, n, k, gs, bits, dtype)
+    x = make_x(rng, 40, k, dtype)
+    rhs = rng.choice(np.array([0, 1, 1, 3, 3, 3, 3, 3], np.uint32), size=rows)  # experts 2, 4 empty
+    lhs = rng.integers(0, 40, size=rows).astype(np.uint32)
+    y = run_gather(device, library, x, w_q, s, b, lhs, rhs, rows, n, k, e, gs, bits, dtype, False)
+    ref = oracle.gather_qmm_ref(x, lhs, rhs, w_q, s, b, rows, n, k, gs, bits, dtype)
+    assert_tol(oracle, y, ref, x, k, dtype, f"gather expert {bits}b K={k}")
 
 
 def test_gather_out_of_range_index_reported(device, library, oracle):
