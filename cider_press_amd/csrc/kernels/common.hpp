@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fastpath.hpp"
+
 namespace cpq {
 namespace dev {
 
@@ -207,58 +209,41 @@ __device__ __forceinline__ float f16hi(uint32_t p) {
   return (float)__builtin_bit_cast(f16x2, p).y;
 }
 
-// Significand width of T (bf16: 8, f16: 11).
 template <typename TT>
-struct Sig;
+struct Sig16;
 template <>
-struct Sig<BF16> {
-  static constexpr int P = 8;
+struct Sig16<BF16> {
+  static constexpr bool bf16 = true;
 };
 template <>
-struct Sig<F16> {
-  static constexpr int P = 11;
+struct Sig16<F16> {
+  static constexpr bool bf16 = false;
 };
 
-// True when c0 = b - 1024*s and c1 = b - 64*s are exact in fp32 and no
-// intermediate can be subnormal: then the fast path equals fmaf(s, q, b).
-template <typename TT>
-__device__ __forceinline__ bool fast_ok(float s, float b) {
-  const uint32_t su = __float_as_uint(s), bu = __float_as_uint(b);
-  const int es = (int)((su >> 23) & 0xffu), eb = (int)((bu >> 23) & 0xffu);
-  if ((su & 0x7fffffffu) == 0u) return (bu & 0x7fffffffu) == 0u || (eb >= 27 && eb < 255);
-  if (es < 27 || es > 240) return false;      // |s| outside [2^-100, 2^113]
-  if ((bu & 0x7fffffffu) == 0u) return true;  // b == 0: c0 = -1024 s, c1 = -64 s
-  if (eb < 27 || eb == 255) return false;
-  constexpr int span = 23 - Sig<TT>::P;
-  const int d0 = eb - (es + 10), d1 = eb - (es + 6);
-  return d0 <= span && d0 >= -span && d1 <= span && d1 >= -span;
-}
-
-// The same predicate on the raw 16-bit patterns of s and b (integer ops only).
-// bf16 (bias 127, 8-bit significand): d = e(b) - e(s) must lie in [-5, 21]
-// (|d-10| <= 15 and |d-6| <= 15) and |s| in [2^-100, 2^113].  f16 (bias 15,
-// 11-bit significand): d in [-2, 18]; every normal f16 is in range.
+// True when the single-FMA fast path reproduces fmaf(s, q, b) for every q
+// of a group with raw scale / bias patterns sv, bv (fastpath.hpp).
 template <typename TT>
 __device__ __forceinline__ bool fast_ok_bits(uint32_t sv, uint32_t bv);
 template <>
 __device__ __forceinline__ bool fast_ok_bits<BF16>(uint32_t sv, uint32_t bv) {
-  const int es = (int)((sv >> 7) & 0xffu), eb = (int)((bv >> 7) & 0xffu);
-  const bool sz = (sv & 0x7fffu) == 0u, bz = (bv & 0x7fffu) == 0u;
-  const bool b_norm = eb >= 27 && eb < 255;
-  if (sz) return bz || b_norm;
-  if (es < 27 || es > 240) return false;
-  const int d = eb - es;
-  return bz || (b_norm && d >= -5 && d <= 21);
+  return fast_ok_bf16(sv, bv);
 }
 template <>
 __device__ __forceinline__ bool fast_ok_bits<F16>(uint32_t sv, uint32_t bv) {
-  const int es = (int)((sv >> 10) & 0x1fu), eb = (int)((bv >> 10) & 0x1fu);
-  const bool sz = (sv & 0x7fffu) == 0u, bz = (bv & 0x7fffu) == 0u;
-  const bool b_norm = eb >= 1 && eb < 31;
-  if (sz) return bz || b_norm;
-  if (es < 1 || es > 30) return false;
-  const int d = eb - es;
-  return bz || (b_norm && d >= -2 && d <= 18);
+  return fast_ok_f16(sv, bv);
+}
+
+// Packed check of two groups per word (sufficient, not necessary: a false
+// result sends the caller to fast_ok_bits for the groups it saw).
+template <typename TT>
+__device__ __forceinline__ void fast_quick_add(FastQuick& a, uint32_t s2, uint32_t b2) {
+  if constexpr (Sig16<TT>::bf16) fast_quick_add_bf16(a, s2, b2);
+  else fast_quick_add_f16(a, s2, b2);
+}
+template <typename TT>
+__device__ __forceinline__ bool fast_quick_ok(const FastQuick& a) {
+  if constexpr (Sig16<TT>::bf16) return fast_quick_ok_bf16(a);
+  else return fast_quick_ok_f16(a);
 }
 
 // Natural 16-byte activation slice -> interleaved slot order of BITS.

@@ -222,13 +222,13 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          ok = ok && fast_ok_bits<TT>(sv[h][q] & 0xffffu, bv[h][q] & 0xffffu) &&
+          ok &= fast_ok_bits<TT>(sv[h][q] & 0xffffu, bv[h][q] & 0xffffu) &
                fast_ok_bits<TT>(sv[h][q] >> 16, bv[h][q] >> 16);
     }
   } else {
     for (int i = tid; i < ncols * G; i += GX_THREADS) {
       const int c = i / G, gi = i - c * G;
-      ok = ok && fast_ok_bits<TT>(se[(size_t)(c0 + c) * G + gi], be[(size_t)(c0 + c) * G + gi]);
+      ok &= fast_ok_bits<TT>(se[(size_t)(c0 + c) * G + gi], be[(size_t)(c0 + c) * G + gi]);
     }
   }
   bool fast = __syncthreads_and(ok);

@@ -355,11 +355,11 @@ __global__ __launch_bounds__(256) void qmm_stream_kernel(const uint32_t* __restr
   // 3. Finish the vote (its loads are older than the stream's).
   bool ok = true;
 #pragma unroll
-  for (int t = 0; t < VOTE_SLOTS; ++t) ok = ok && fast_ok_bits<TT>(vs[t], vb[t]);
+  for (int t = 0; t < VOTE_SLOTS; ++t) ok &= fast_ok_bits<TT>(vs[t], vb[t]);
   for (int i = tid + 256 * VOTE_SLOTS; i < vcount; i += 256) {
     const int cc = min(col0 + i / G, n - 1);
     const size_t off = (size_t)cc * G + (i % G);
-    ok = ok && fast_ok_bits<TT>(scales[off], biases[off]);
+    ok &= fast_ok_bits<TT>(scales[off], biases[off]);
   }
   const bool fast = __syncthreads_and(ok);
 
@@ -640,7 +640,7 @@ __global__ __launch_bounds__(256 * MH) __attribute__((amdgpu_waves_per_eu(MH, MH
   uint32_t* cst = reinterpret_cast<uint32_t*>(smem + cst_base);
   bool ok = true;
   auto put = [&](int c, int gi, uint32_t sv, uint32_t bv) {
-    ok = ok && fast_ok_bits<TT>(sv, bv);
+    ok &= fast_ok_bits<TT>(sv, bv);
     cst[(gi * 16 + (c & 15)) * 4 + (c >> 4)] = sv | (bv << 16);
   };
   if (sb_vec) {

@@ -93,13 +93,27 @@ __device__ __forceinline__ f32x4 stream(const QmvGeom& q, int nsteps, uint32_t (
   return acc;
 }
 
-constexpr int kSegSlots = 2;  // 16-B scale/bias segments held per thread before the weight loads
+constexpr int kSegSlots = 2;  // 8-B scale/bias quads held per thread before the weight loads
 constexpr int kXSlots = 4;    // 16-B activation slices held per thread before the weight loads
 
 template <typename TT>
 __device__ __forceinline__ f32x4 group_consts(uint32_t sv, uint32_t bv) {
   const float s = TT::to_f32((uint16_t)sv), b = TT::to_f32((uint16_t)bv);
   return f32x4{s, b, fmaf(-1024.f, s, b), fmaf(-64.f, s, b)};
+}
+
+// One chunk (BITS words) of a weight row through a buffer descriptor.
+template <int BITS>
+__device__ __forceinline__ void lean_load(__amdgpu_buffer_rsrc_t wr, uint32_t voff, int soff, uint32_t* dst) {
+  if constexpr (BITS == 4) {
+    const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff, soff, 0));
+    dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+  } else {
+    const u32x4 v0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff, soff, 0));
+    const u32x4 v1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff + 16, soff, 0));
+    dst[0] = v0.x; dst[1] = v0.y; dst[2] = v0.z; dst[3] = v0.w;
+    dst[4] = v1.x; dst[5] = v1.y; dst[6] = v1.z; dst[7] = v1.w;
+  }
 }
 
 template <typename TT, int BITS, int WAVES, int PF, bool EXACT>
@@ -137,20 +151,21 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_kernel(const uint32_t* __restr
   q.u_end = min(units, q.u0 + per_wave);
   const int nsteps = (per_wave + PF - 1) / PF * PF;
 
-  // 1. Small loads first: (scale, bias) segments of the 16 rows, activation.
-  const bool vec = (G & 7) == 0 &&
-                   ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(biases)) & 15u) == 0;
-  const int segs = G >> 3;
-  u32x4 sv[kSegSlots], bv[kSegSlots];
+  // 1. Small loads first: (scale, bias) quads (4 groups, 8 B) of the 16 rows,
+  //    then the activation.
+  const bool vec = (G & 3) == 0 &&
+                   ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(biases)) & 7u) == 0;
+  const int quads = G >> 2;
+  u32x2 sv[kSegSlots], bv[kSegSlots];
 #pragma unroll
   for (int t = 0; t < kSegSlots; ++t) {
     const int i = tid + t * NT;
-    sv[t] = bv[t] = u32x4{0u, 0u, 0u, 0u};
-    if (vec && i < 16 * segs) {
-      const int r = i / segs, sg = i - r * segs;
+    sv[t] = bv[t] = u32x2{0u, 0u};
+    if (vec && i < 16 * quads) {
+      const int r = i / quads, sg = i - r * quads;
       if (n0 + r < n) {
-        sv[t] = *reinterpret_cast<const u32x4*>(scales + (size_t)(n0 + r) * G + sg * 8);
-        bv[t] = *reinterpret_cast<const u32x4*>(biases + (size_t)(n0 + r) * G + sg * 8);
+        sv[t] = *reinterpret_cast<const u32x2*>(scales + (size_t)(n0 + r) * G + sg * 4);
+        bv[t] = *reinterpret_cast<const u32x2*>(biases + (size_t)(n0 + r) * G + sg * 4);
       }
     }
   }
@@ -167,8 +182,9 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_kernel(const uint32_t* __restr
 #pragma unroll
   for (int p = 0; p < PF; ++p) fetch<BITS, EXACT>(q, p, buf[p]);
 
-  // 3. Stage to LDS (and anything beyond the register slots), vote.
-  bool ok = true;
+  // 3. Stage to LDS (and anything beyond the register slots), vote: one
+  //    packed check over all of this thread's groups, the exact per-group
+  //    predicate only where the packed check fails (zero scales or biases).
 #pragma unroll
   for (int t = 0; t < kXSlots; ++t) {
     const int i = tid + t * NT;
@@ -178,35 +194,49 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_kernel(const uint32_t* __restr
     const u32x4 v = *reinterpret_cast<const u32x4*>(x + (size_t)i * 8);
     *reinterpret_cast<u32x4*>(xs + (size_t)i * 8) = interleave_x<BITS>(v);
   }
+  bool ok = true;
   if (vec) {
+    FastQuick fq;
+    fast_quick_init(fq);
 #pragma unroll
     for (int t = 0; t < kSegSlots; ++t) {
       const int i = tid + t * NT;
-      if (i < 16 * segs) {
-        const int r = i / segs, sg = i - r * segs;
-        f32x4* dst = gct + r * GP + sg * 8;
+      if (i < 16 * quads) {
+        const int r = i / quads, sg = i - r * quads;
+        f32x4* dst = gct + r * GP + sg * 4;
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
+        for (int h = 0; h < 2; ++h) {
           const uint32_t s2 = sv[t][h], b2 = bv[t][h];
           dst[2 * h] = group_consts<TT>(s2 & 0xffffu, b2 & 0xffffu);
           dst[2 * h + 1] = group_consts<TT>(s2 >> 16, b2 >> 16);
-          ok = ok && fast_ok_bits<TT>(s2 & 0xffffu, b2 & 0xffffu) && fast_ok_bits<TT>(s2 >> 16, b2 >> 16);
+          fast_quick_add<TT>(fq, s2, b2);
         }
       }
     }
-    for (int i = tid + kSegSlots * NT; i < 16 * segs; i += NT) {
-      const int r = i / segs, sg = i - r * segs;
-      u32x4 s4 = {0u, 0u, 0u, 0u}, b4 = {0u, 0u, 0u, 0u};
-      if (n0 + r < n) {
-        s4 = *reinterpret_cast<const u32x4*>(scales + (size_t)(n0 + r) * G + sg * 8);
-        b4 = *reinterpret_cast<const u32x4*>(biases + (size_t)(n0 + r) * G + sg * 8);
-      }
-      f32x4* dst = gct + r * GP + sg * 8;
+    if (!fast_quick_ok<TT>(fq)) {
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
+      for (int t = 0; t < kSegSlots; ++t) {
+        if (tid + t * NT < 16 * quads) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            ok &= fast_ok_bits<TT>(sv[t][h] & 0xffffu, bv[t][h] & 0xffffu) &
+                  fast_ok_bits<TT>(sv[t][h] >> 16, bv[t][h] >> 16);
+        }
+      }
+    }
+    for (int i = tid + kSegSlots * NT; i < 16 * quads; i += NT) {
+      const int r = i / quads, sg = i - r * quads;
+      u32x2 s4 = {0u, 0u}, b4 = {0u, 0u};
+      if (n0 + r < n) {
+        s4 = *reinterpret_cast<const u32x2*>(scales + (size_t)(n0 + r) * G + sg * 4);
+        b4 = *reinterpret_cast<const u32x2*>(biases + (size_t)(n0 + r) * G + sg * 4);
+      }
+      f32x4* dst = gct + r * GP + sg * 4;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
         dst[2 * h] = group_consts<TT>(s4[h] & 0xffffu, b4[h] & 0xffffu);
         dst[2 * h + 1] = group_consts<TT>(s4[h] >> 16, b4[h] >> 16);
-        ok = ok && fast_ok_bits<TT>(s4[h] & 0xffffu, b4[h] & 0xffffu) && fast_ok_bits<TT>(s4[h] >> 16, b4[h] >> 16);
+        ok &= fast_ok_bits<TT>(s4[h] & 0xffffu, b4[h] & 0xffffu) & fast_ok_bits<TT>(s4[h] >> 16, b4[h] >> 16);
       }
     }
   } else {
@@ -218,7 +248,7 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_kernel(const uint32_t* __restr
         b1 = biases[(size_t)(n0 + r) * G + gi];
       }
       gct[r * GP + gi] = group_consts<TT>(s1, b1);
-      ok = ok && fast_ok_bits<TT>(s1, b1);
+      ok &= fast_ok_bits<TT>(s1, b1);
     }
   }
   const bool fast = __syncthreads_and(ok);
@@ -229,6 +259,187 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_kernel(const uint32_t* __restr
 
   // D[m][n] sits in lane n + 16*(m/4), element m%4; every A row holds x, so
   // lanes 0..15 element 0 carry row n0 + lane.
+  if (lane < 16) red[wave * 16 + lane] = acc[0];
+  __syncthreads();
+  if (tid < 16 && n0 + tid < n) {
+    float v = 0.f;
+#pragma unroll
+    for (int i = 0; i < WAVES; ++i) v += red[i * 16 + tid];
+    y[n0 + tid] = TT::from_f32(v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Lean decode kernel (4/8-bit, K % 2048 == 0, gs in {32, 64, 128}).
+//
+// Same work split as qmv_kernel (16 rows per workgroup, K split over 4 waves,
+// lane = (row l%16, chunk 4u + l/16)), but every wave is self-contained until
+// the final sum, and its fixed work is cut to a few dozen instructions so the
+// VALU time goes to dequantization:
+//   - a wave loads and stages only what its own K range needs (its 16 x 16B
+//     activation items per step batch, the constants of its own groups) into
+//     a private LDS region, votes for the fast path within the wave, and
+//     starts streaming without waiting for the other waves;
+//   - every global access is a buffer load: per-step offsets are immediates
+//     or one scalar, rows past N read zeros (range-checked by the
+//     descriptor), so there are no per-load address computations and no
+//     bounds branches;
+//   - the group constants and activation slices of step j sit at immediate
+//     LDS offsets from one per-lane base (gs is a template parameter).
+// ---------------------------------------------------------------------------
+constexpr int kLeanXItems = 8;   // 16-B activation items per lane (K <= 16384)
+constexpr int kLeanQuads = 8;    // 8-B scale/bias quads per lane (wave's groups per row <= 128)
+
+// Per-wave LDS: activations (256 B per step) then constants [16][GW + 1].
+__host__ __device__ constexpr size_t lean_wave_lds(int nsteps, int gs_shift) {
+  return (size_t)256 * nsteps + (size_t)16 * ((size_t)nsteps * (128 >> gs_shift) + 1) * 16;
+}
+
+template <typename TT, int BITS, int GS_SHIFT, int PF, bool ONE, bool FAST>
+__device__ __forceinline__ f32x4 lean_stream(__amdgpu_buffer_rsrc_t wr, uint32_t voff, int nsteps,
+                                             const unsigned char* cbase, const unsigned char* xbase,
+                                             uint32_t (&buf)[PF][BITS]) {
+  constexpr int CB = BITS * 4;             // bytes per 32-element chunk
+  constexpr int STEP_W = 4 * CB;           // weight bytes a lane group advances per step
+  constexpr int STEP_C = (128 >> GS_SHIFT) * 16;  // constants bytes per step
+  constexpr int STEP_X = 4 * 64;           // activation bytes per step (4 chunks x 32 x 2 B)
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  auto step = [&](const uint32_t* cur, int j) {
+    const f32x4 gc = *reinterpret_cast<const f32x4*>(cbase + j * STEP_C);
+    const u32x4* xa = reinterpret_cast<const u32x4*>(xbase + j * STEP_X);
+    const float sc = gc[0], b = gc[1], c0 = gc[2], c1 = gc[3];
+    const float s16 = sc * 0.0625f;
+    acc = Mfma16<TT>::run(xa[0], dequant_slice<TT, BITS, FAST, 0>(cur, sc, s16, b, c0, c1), acc);
+    acc = Mfma16<TT>::run(xa[1], dequant_slice<TT, BITS, FAST, 1>(cur, sc, s16, b, c0, c1), acc);
+    acc = Mfma16<TT>::run(xa[2], dequant_slice<TT, BITS, FAST, 2>(cur, sc, s16, b, c0, c1), acc);
+    acc = Mfma16<TT>::run(xa[3], dequant_slice<TT, BITS, FAST, 3>(cur, sc, s16, b, c0, c1), acc);
+  };
+  int base = 0;
+  // ONE: the whole range is the PF prefetched steps (no loop, buffers consumed in place).
+  for (; !ONE && base + PF < nsteps; base += PF) {
+    const int soff = (base + PF) * STEP_W;
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      uint32_t cur[BITS];
+#pragma unroll
+      for (int i = 0; i < BITS; ++i) cur[i] = buf[p][i];
+      lean_load<BITS>(wr, voff + p * STEP_W, soff, buf[p]);
+      step(cur, base + p);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < PF; ++p) step(buf[p], base + p);
+  return acc;
+}
+
+template <typename TT, int BITS, int GS_SHIFT, int WAVES, int PF, bool ONE>
+__global__ __launch_bounds__(64 * WAVES) void qmv_lean_kernel(const uint32_t* __restrict__ w,
+                                                                   const uint16_t* __restrict__ scales,
+                                                                   const uint16_t* __restrict__ biases,
+                                                                   const uint16_t* __restrict__ x,
+                                                                   uint16_t* __restrict__ y, int n, int k) {
+  constexpr int CB = BITS * 4;
+  constexpr int GPS = 128 >> GS_SHIFT;  // groups per step (4 chunks of 32)
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int G = k >> GS_SHIFT;
+  const int nsteps = ONE ? PF : k / (128 * WAVES);  // steps per wave: K / (32 * 4 * waves)
+  const int GW = nsteps * GPS;          // groups of one row in this wave's K range
+  const int quads = GW >> 2;            // 8-B quads of one row in this wave's K range
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int u0 = wave * nsteps;         // first step unit of this wave
+  const uint32_t rowbytes = (uint32_t)k * BITS / 8;
+  unsigned char* xw = smem + (size_t)wave * lean_wave_lds(nsteps, GS_SHIFT);
+  f32x4* cw = reinterpret_cast<f32x4*>(xw + (size_t)256 * nsteps);  // [16][GW + 1]
+  float* red = reinterpret_cast<float*>(smem + (size_t)WAVES * lean_wave_lds(nsteps, GS_SHIFT));
+
+  const __amdgpu_buffer_rsrc_t wr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)w, 0, (int)((uint32_t)n * rowbytes), 0x00020000);
+  const __amdgpu_buffer_rsrc_t sr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)scales, 0, (int)((uint32_t)n * (uint32_t)G * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t br =
+      __builtin_amdgcn_make_buffer_rsrc((void*)biases, 0, (int)((uint32_t)n * (uint32_t)G * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)x, 0, k * 2, 0x00020000);
+
+  // 1. Small loads first: this wave's scale / bias quads (row lane/4, quad
+  //    lane%4 + 4t) and its activation items (lane + 64t of its range).
+  const int cr = lane >> 2;
+  const uint32_t coff = ((uint32_t)(n0 + cr) * (uint32_t)G + (uint32_t)(u0 * GPS + 4 * (lane & 3))) * 2u;
+  u32x2 sv[kLeanQuads], bv[kLeanQuads];
+#pragma unroll
+  for (int t = 0; t < kLeanQuads; ++t) {
+    sv[t] = bv[t] = u32x2{0u, 0u};
+    if (4 * t < quads) {
+      sv[t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(sr, coff + 32u * t, 0, 0));
+      bv[t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(br, coff + 32u * t, 0, 0));
+    }
+  }
+  const int xitems = 4 * nsteps;  // 16-B items of this wave per 16 lanes... per lane: nsteps / 4
+  const uint32_t xoff = (uint32_t)u0 * 256u + (uint32_t)lane * 16u;
+  u32x4 xv[kLeanXItems];
+#pragma unroll
+  for (int t = 0; t < kLeanXItems; ++t) {
+    xv[t] = u32x4{0u, 0u, 0u, 0u};
+    if (4 * t < nsteps)
+      xv[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + 1024u * t, 0, 0));
+  }
+  (void)xitems;
+
+  // 2. The weight stream: lane (r, g) reads chunk 4(u0 + j) + g of row n0 + r.
+  const uint32_t voff = (uint32_t)(n0 + r) * rowbytes + (uint32_t)(4 * u0 + g) * CB;
+  uint32_t buf[PF][BITS];
+#pragma unroll
+  for (int p = 0; p < PF; ++p) lean_load<BITS>(wr, voff + p * 4 * CB, 0, buf[p]);
+
+  // 3. Stage this wave's activations and constants, vote within the wave.
+#pragma unroll
+  for (int t = 0; t < kLeanXItems; ++t)
+    if (4 * t < nsteps) *reinterpret_cast<u32x4*>(xw + lane * 16 + 1024 * t) = interleave_x<BITS>(xv[t]);
+  FastQuick fq;
+  fast_quick_init(fq);
+  const int cwp = GW + 1;
+#pragma unroll
+  for (int t = 0; t < kLeanQuads; ++t) {
+    const int cq = (lane & 3) + 4 * t;
+    if (4 * t < quads && cq < quads) {
+      f32x4* dst = cw + cr * cwp + cq * 4;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        dst[2 * h] = group_consts<TT>(sv[t][h] & 0xffffu, bv[t][h] & 0xffffu);
+        dst[2 * h + 1] = group_consts<TT>(sv[t][h] >> 16, bv[t][h] >> 16);
+        fast_quick_add<TT>(fq, sv[t][h], bv[t][h]);
+      }
+    }
+  }
+  bool ok = true;
+  if (!fast_quick_ok<TT>(fq)) {
+#pragma unroll
+    for (int t = 0; t < kLeanQuads; ++t) {
+      const int cq = (lane & 3) + 4 * t;
+      if (4 * t < quads && cq < quads) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          ok &= fast_ok_bits<TT>(sv[t][h] & 0xffffu, bv[t][h] & 0xffffu) &
+                fast_ok_bits<TT>(sv[t][h] >> 16, bv[t][h] >> 16);
+      }
+    }
+  }
+  // Lanes of one wave read each other's LDS writes: order them within the wave.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const bool fast = __builtin_amdgcn_ballot_w64(!ok) == 0;
+
+  // 4. Stream.  Step j of this lane: constants of local group j*GPS + (32g >> GS_SHIFT),
+  //    activation chunk 4j + g of the wave's range; both advance by fixed bytes per step.
+  const unsigned char* cbase = reinterpret_cast<const unsigned char*>(cw + r * cwp + ((g * 32) >> GS_SHIFT));
+  const unsigned char* xbase = xw + g * 64;
+  const f32x4 acc = fast ? lean_stream<TT, BITS, GS_SHIFT, PF, ONE, true>(wr, voff, nsteps, cbase, xbase, buf)
+                         : lean_stream<TT, BITS, GS_SHIFT, PF, ONE, false>(wr, voff, nsteps, cbase, xbase, buf);
+
   if (lane < 16) red[wave * 16 + lane] = acc[0];
   __syncthreads();
   if (tid < 16 && n0 + tid < n) {
@@ -280,10 +491,75 @@ hipError_t launch_pf(hipStream_t s, const QuantArgs& q, const void* x, void* y, 
   return launch_cfg<TT, BITS, WAVES, PF, false>(s, q, x, y, n, k, lds);
 }
 
+template <typename TT, int BITS, int GS_SHIFT, int WAVES, int PF, bool ONE>
+hipError_t launch_lean_cfg(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k,
+                           size_t lds) {
+  if (lds > 64 * 1024) {
+    static const hipError_t attr = [] {
+      const void* fn = reinterpret_cast<const void*>(&qmv_lean_kernel<TT, BITS, GS_SHIFT, WAVES, PF, ONE>);
+      hipFuncAttributes fa;
+      hipError_t e = hipFuncGetAttributes(&fa, fn);
+      if (e != hipSuccess) return e;
+      return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)(160 * 1024 - fa.sharedSizeBytes));
+    }();
+    if (attr != hipSuccess) return attr;
+  }
+  hipLaunchKernelGGL((qmv_lean_kernel<TT, BITS, GS_SHIFT, WAVES, PF, ONE>), dim3((unsigned)((n + 15) / 16)),
+                     dim3(64 * WAVES), lds, s, q.w, static_cast<const uint16_t*>(q.scales),
+                     static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x),
+                     static_cast<uint16_t*>(y), n, k);
+  return hipGetLastError();
+}
+
+template <typename TT, int BITS, int GS_SHIFT, int WAVES>
+hipError_t launch_lean_gs(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k,
+                          size_t lds) {
+  const int nsteps = k / (128 * WAVES);
+  if (nsteps == 8) return launch_lean_cfg<TT, BITS, GS_SHIFT, WAVES, 8, true>(s, q, x, y, n, k, lds);
+  if (nsteps == 4) return launch_lean_cfg<TT, BITS, GS_SHIFT, WAVES, 4, true>(s, q, x, y, n, k, lds);
+  if (nsteps % 8 == 0) return launch_lean_cfg<TT, BITS, GS_SHIFT, WAVES, 8, false>(s, q, x, y, n, k, lds);
+  return launch_lean_cfg<TT, BITS, GS_SHIFT, WAVES, 4, false>(s, q, x, y, n, k, lds);
+}
+
+template <typename TT, int BITS, int WAVES>
+hipError_t launch_lean_w(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k,
+                         size_t lds) {
+  if (q.gs == 32) return launch_lean_gs<TT, BITS, 5, WAVES>(s, q, x, y, n, k, lds);
+  if (q.gs == 64) return launch_lean_gs<TT, BITS, 6, WAVES>(s, q, x, y, n, k, lds);
+  return launch_lean_gs<TT, BITS, 7, WAVES>(s, q, x, y, n, k, lds);
+}
+
+// The lean kernel's shape contract: K a multiple of 512 * waves (each wave a
+// whole number of 4-step batches), at most 16384 activations and 128 groups
+// per row in one wave's K range, 32-bit buffer ranges, 8-byte aligned scales
+// and biases.
+template <int BITS>
+bool lean_fits(const QuantArgs& q, int n, int k, int waves) {
+  if (BITS != 4 && BITS != 8) return false;
+  if (q.gs != 32 && q.gs != 64 && q.gs != 128) return false;
+  if (k % (512 * waves) != 0 || k > 16384 || (k / waves) / q.gs > 4 * kLeanQuads * 4) return false;
+  if ((uint64_t)n * (uint64_t)k * BITS / 8 >= (1ull << 31)) return false;
+  if ((uint64_t)n * (uint64_t)(k / q.gs) * 2 >= (1ull << 31)) return false;
+  return ((reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases)) & 7u) == 0;
+}
+
 template <typename TT, int BITS>
 hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k) {
   const size_t G = (size_t)k / q.gs;
   const size_t lds = (size_t)k * 2 + 16 * (G + 1) * 16 + 8 * 16 * 4;
+  if constexpr (BITS == 4 || BITS == 8) {
+    // Few row blocks (under two per CU): 8 waves per block keep two waves per SIMD.
+    const int waves = (n + 15) / 16 < 512 && lean_fits<BITS>(q, n, k, 8) ? 8 : 4;
+    if (lean_fits<BITS>(q, n, k, waves)) {
+      const int sh = shift_of(q.gs);
+      const size_t llds = (size_t)waves * lean_wave_lds(k / (128 * waves), sh) + (size_t)waves * 16 * 4;
+      if (llds <= 160 * 1024 - 1024) {
+        if (waves == 8) return launch_lean_w<TT, BITS, 8>(s, q, x, y, n, k, llds);
+        return launch_lean_w<TT, BITS, 4>(s, q, x, y, n, k, llds);
+      }
+    }
+  }
   if (lds > 160 * 1024)  // very long rows: the LDS-free small-M kernel
     return launch_qmm_skinny(s, q, x, y, 1, n, k);
   const int units = k / 128;

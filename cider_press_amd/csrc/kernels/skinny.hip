@@ -79,7 +79,7 @@ __device__ __forceinline__ bool slab_consts_store(const uint16_t* __restrict__ s
                                                   int GP) {
   bool ok = true;
   auto put = [&](int c, int gi, uint32_t sv, uint32_t bv) {
-    ok = ok && fast_ok_bits<TT>(sv, bv);
+    ok &= fast_ok_bits<TT>(sv, bv);
     const float sf = TT::to_f32((uint16_t)sv), bf = TT::to_f32((uint16_t)bv);
     gc[c * GP + gi] = f32x4{sf, bf, fmaf(-1024.f, sf, bf), fmaf(-64.f, sf, bf)};
   };

@@ -9,6 +9,7 @@
 // the same; "kernel not found" is reported after shape validation, as the
 // reference's pipeline lookup is (qmv.rs:172-173, library.rs:264-286).
 #include <climits>
+#include <cstdlib>
 #include <string>
 
 #include "cpq_internal.hpp"
@@ -22,11 +23,18 @@ bool kernel_available(cpq_dtype dtype, uint32_t group_size, uint32_t bits) {
   return t_ok && gs_ok && b_ok;
 }
 
+// Largest M the routed op sends to the small-M kernel (one 16-column slab of W
+// per workgroup, up to 64 activation rows per pass).  CPQ_SKINNY_MAX_M
+// overrides it, read once per process.
 int skinny_max_m(const QuantArgs& q, int n, int k) {
   (void)q;
   (void)n;
   (void)k;
-  return 32;
+  static const int lim = [] {
+    const char* e = std::getenv("CPQ_SKINNY_MAX_M");
+    return e && *e ? std::atoi(e) : 32;
+  }();
+  return lim;
 }
 
 namespace {
