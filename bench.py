@@ -48,7 +48,7 @@ BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic.json")
 COPY_BYTES = 512 << 20         # calibration copy: 512 MiB read + 512 MiB written
 QMV_KERNEL = "qmv_lean_kernel<cpq::dev::BF16, 4"
-QMM_KERNEL = "qmm_staged_kernel<cpq::dev::BF16, 4"
+QMM_KERNEL = "qmm_wide_kernel<cpq::dev::BF16"
 COPY_KERNEL = "copy"
 
 

@@ -26,6 +26,7 @@ SOURCES = [
     "kernels/qmv.hip",
     "kernels/skinny.hip",
     "kernels/qmm.hip",
+    "kernels/qmm_wide.hip",
     "kernels/gather.hip",
 ]
 

@@ -7,6 +7,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "../../include/cpq.h"
 
@@ -27,6 +28,13 @@ struct cpq_commands {
   // Device-side status word: kernels that can detect bad data (gather indices)
   // add to it; cpq_commands_wait reads and clears it.
   unsigned int* status = nullptr;
+  // Split-K scratch of the prefill kernel: arrival counters (zero between
+  // launches) followed by fp32 partial tiles.  Grown only outside graph
+  // capture; replaced blocks stay allocated until the session is released,
+  // since a captured graph may still use them.
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
+  std::vector<void*> scratch_retired;
 };
 
 struct cpq_event {
@@ -73,8 +81,25 @@ hipError_t launch_qmm_skinny(hipStream_t s, const QuantArgs& q, const void* x, v
                              int n, int k);
 
 // Prefill GEMM: LDS-tiled bf16/f16 MFMA with the W tile dequantized into LDS.
-hipError_t launch_qmm(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n,
+// Uses the session's stream, and its split-K scratch when K is split.
+hipError_t launch_qmm(cpq_commands* cmds, const QuantArgs& q, const void* x, void* y, int m, int n,
                       int k);
+
+// Wide-tile prefill kernel (4-bit, 128 x 128 tiles, optional split K).
+constexpr size_t kWideCounterBytes = 64 * 1024;  // arrival counters at the head of the scratch
+bool qmm_wide_fits(int m, int n, int k, int gs, int bits, int split);
+// Split (1, 2 or 4) that minimises the estimated makespan; 0 if the kernel
+// does not apply.
+int qmm_wide_split(int m, int n, int k, int gs, int bits, int cu_count);
+size_t qmm_wide_scratch_bytes(int m, int n, int split);
+hipError_t launch_qmm_wide(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n,
+                           int k, int split, void* scratch);
+hipError_t zero_words(hipStream_t s, void* p, size_t n_words);
+
+// At least `bytes` of the session's split-K scratch (counters zeroed).
+// Fails with hipErrorStreamCaptureUnsupported when it would have to grow
+// while the stream is being captured.
+hipError_t session_scratch(cpq_commands* cmds, size_t bytes, void** out);
 
 // Routed experts, expert-major kernel (4/8-bit, K % 128 == 0): one
 // workgroup per (expert, column chunk).  gather_expert_supported says whether

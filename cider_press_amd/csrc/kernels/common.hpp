@@ -363,6 +363,15 @@ struct Mfma16<F16> {
   }
 };
 
+// Wait until at most N vector-memory loads of this wave are outstanding
+// (loads complete in issue order, so this proves every older load done).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  // s_waitcnt simm16 (gfx9): vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] at [15:14].
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 // Wave64 sum via DPP-friendly butterfly.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

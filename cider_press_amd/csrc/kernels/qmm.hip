@@ -18,6 +18,8 @@
 // register 4*(m/8) + m%4.
 #include <algorithm>
 
+#include <cstdlib>
+
 #include "../cpq_internal.hpp"
 #include "common.hpp"
 
@@ -501,13 +503,6 @@ constexpr int stage_vmcnt() {
   }
 }
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N <= 63, "vmcnt range");
-  // s_waitcnt simm16 (gfx9): vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] at [15:14].
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
 // Stage s = s0 + P.  On entry a[P & 1] holds stage s's A fragments and bop
 // its B operands.  The stage proves stage s+1's copies complete (own vmcnt,
 // then the barrier for the other waves'), refills the slot of stage s-1
@@ -821,8 +816,36 @@ hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, i
 
 }  // namespace
 
-hipError_t launch_qmm(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n,
+namespace {
+
+// CPQ_QMM_WIDE=0 turns the wide-tile kernel off; CPQ_QMM_SPLIT=1|2|4 forces
+// its K split.  Both are read per call (test and tuning hooks).
+int env_int(const char* name, int dflt) {
+  const char* e = std::getenv(name);
+  return e && *e ? std::atoi(e) : dflt;
+}
+
+}  // namespace
+
+hipError_t launch_qmm(cpq_commands* cmds, const QuantArgs& q, const void* x, void* y, int m, int n,
                       int k) {
+  hipStream_t s = cmds->stream;
+  const bool sb16 = ((reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases)) & 15u) == 0;
+  if (q.bits == 4 && sb16 && env_int("CPQ_QMM_WIDE", 1) != 0) {
+    const int forced = env_int("CPQ_QMM_SPLIT", 0);
+    int split = forced > 0 ? (qmm_wide_fits(m, n, k, q.gs, q.bits, forced) ? forced : 0)
+                           : qmm_wide_split(m, n, k, q.gs, q.bits, cmds->dev ? cmds->dev->cu_count : 0);
+    // A split needs session scratch; if it cannot grow (graph capture), try
+    // smaller splits.
+    for (; split > 1; split /= 2) {
+      if (!qmm_wide_fits(m, n, k, q.gs, q.bits, split)) continue;
+      void* scratch = nullptr;
+      if (session_scratch(cmds, qmm_wide_scratch_bytes(m, n, split), &scratch) == hipSuccess)
+        return launch_qmm_wide(s, q, x, y, m, n, k, split, scratch);
+    }
+    if (split == 1 && qmm_wide_fits(m, n, k, q.gs, q.bits, 1))
+      return launch_qmm_wide(s, q, x, y, m, n, k, 1, nullptr);
+  }
 #define CPQ_QMM_BITS(TT)                                   \
   switch (q.bits) {                                        \
     case 2: return launch_t<TT, 2>(s, q, x, y, m, n, k);   \

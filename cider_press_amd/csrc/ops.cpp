@@ -315,7 +315,7 @@ cpq_status cpq_affine_qmm_t(cpq_commands* cmds, cpq_dtype dtype, const uint32_t*
   st = cpq::check_ptrs("affine_qmm_t", w_q, scales, biases, x, y);
   if (st != CPQ_OK) return st;
   cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
-  return cpq::launched(cpq::launch_qmm(cmds->stream, q, x, y, (int)m, (int)n, (int)k),
+  return cpq::launched(cpq::launch_qmm(cmds, q, x, y, (int)m, (int)n, (int)k),
                        "affine_qmm_t launch");
 }
 
@@ -387,7 +387,7 @@ cpq_status cpq_quantized_matmul(cpq_commands* cmds, cpq_dtype dtype, const uint3
   if ((long)m <= cpq::skinny_max_m(q, (int)n, (int)k_physical))
     return cpq::launched(cpq::launch_qmm_skinny(cmds->stream, q, x, y, (int)m, (int)n, (int)k_physical),
                          "quantized_matmul (small-M) launch");
-  return cpq::launched(cpq::launch_qmm(cmds->stream, q, x, y, (int)m, (int)n, (int)k_physical),
+  return cpq::launched(cpq::launch_qmm(cmds, q, x, y, (int)m, (int)n, (int)k_physical),
                        "quantized_matmul (prefill) launch");
 }
 

@@ -6,7 +6,9 @@
 // hipMalloc'd device memory instead of shared MTLBuffers.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -28,6 +30,35 @@ cpq_status hip_fail(hipError_t e, const char* what) {
   std::string m = std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
   g_last_error = m;
   return CPQ_ERR_HIP_API;
+}
+
+hipError_t session_scratch(cpq_commands* c, size_t bytes, void** out) {
+  if (bytes <= c->scratch_bytes) {
+    *out = c->scratch;
+    return hipSuccess;
+  }
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(c->stream, &cs);
+  if (e != hipSuccess) return e;
+  if (cs != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
+  const size_t mib = size_t(1) << 20;
+  size_t want = std::max(bytes, 2 * c->scratch_bytes);
+  want = (want + mib - 1) / mib * mib;
+  void* p = nullptr;
+  e = hipMalloc(&p, want);
+  if (e != hipSuccess) return e;
+  // Counters start at zero; a kernel (not a memset) so the stream stays
+  // free of memset nodes should it be captured later.
+  e = zero_words(c->stream, p, kWideCounterBytes / 4);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return e;
+  }
+  if (c->scratch) c->scratch_retired.push_back(c->scratch);
+  c->scratch = p;
+  c->scratch_bytes = want;
+  *out = p;
+  return hipSuccess;
 }
 
 }  // namespace cpq
@@ -184,6 +215,17 @@ static cpq_status make_commands(cpq_device* dev, hipStream_t stream, bool owns,
   c->stream = stream;
   c->owns_stream = owns;
   c->status = status;
+  // Split-K scratch for the prefill kernel, sized up front (CPQ_SESSION_SCRATCH_MB,
+  // default 64 MiB: 1024 partial tiles) so that a session whose first calls
+  // are captured into a graph still finds it.  Failure is not an error: the
+  // prefill path then runs unsplit.
+  const char* env = std::getenv("CPQ_SESSION_SCRATCH_MB");
+  const long mb = env && *env ? std::atol(env) : 64;
+  if (mb > 0) {
+    void* p = nullptr;
+    (void)cpq::session_scratch(c, (size_t)mb << 20, &p);
+    (void)hipGetLastError();
+  }
   *out = c;
   return CPQ_OK;
 }
@@ -243,6 +285,8 @@ void cpq_commands_release(cpq_commands* cmds) {
   if (!cmds) return;
   if (cmds->stream) (void)hipStreamSynchronize(cmds->stream);
   if (cmds->status) (void)hipFree(cmds->status);
+  if (cmds->scratch) (void)hipFree(cmds->scratch);
+  for (void* p : cmds->scratch_retired) (void)hipFree(p);
   if (cmds->owns_stream && cmds->stream) (void)hipStreamDestroy(cmds->stream);
   delete cmds;
 }

@@ -242,6 +242,75 @@ def test_quantized_matmul_routes_all_m(device, library, oracle, m, bits, gs):
     assert_tol(oracle, y, ref, x, k, "bf16", f"routed m={m}")
 
 
+# The 4-bit prefill path runs the wide-tile kernel (128 x 128 tiles, K split
+# over 1, 2 or 4 workgroups, partial tiles summed by the last to finish);
+# CPQ_QMM_SPLIT forces the split, CPQ_QMM_WIDE=0 the earlier staged kernel.
+@pytest.mark.parametrize("m,n,k,gs,dtype,split", [
+    (256, 512, 2048, 64, "bf16", 1),
+    (256, 512, 2048, 64, "bf16", 2),
+    (512, 4096, 4096, 64, "bf16", 2),      # config 3a
+    (300, 640, 4096, 32, "bf16", 4),       # ragged M
+    (200, 352, 4096, 64, "f16", 2),        # ragged M and a partial column tile
+    (200, 352, 4096, 64, "f16", 4),
+    (129, 256, 2048, 128, "bf16", 1),
+    (129, 256, 2048, 128, "bf16", 2),
+    (64, 4096, 4096, 64, "bf16", 4),       # config 4 at M = 64
+])
+def test_qmm_wide_parity(device, library, oracle, monkeypatch, m, n, k, gs, dtype, split):
+    monkeypatch.setenv("CPQ_QMM_SPLIT", str(split))
+    rng = np.random.default_rng(m + n + split)
+    w_q, s, b = make_weight(rng, n, k, gs, 4, dtype)
+    x = make_x(rng, m, k, dtype)
+    y = run_qmm(device, library, w_q, s, b, x, m, n, k, gs, 4, dtype)
+    ref = oracle.qmm_ref(x, w_q, s, b, m, n, k, gs, 4, dtype)
+    assert_tol(oracle, y, ref, x, k, dtype, f"wide split={split} {m}x{n}x{k}")
+
+
+# Scale / bias pairs outside the single-FMA fast path's exactness range: a
+# tiny scale under a much larger bias (bf16 exponent gap 24), or an f16
+# subnormal scale.  Their column tile takes the generic dequantization; the
+# other tiles stay fast.
+_SLOW_SB = {"bf16": (0x3000, 0x3C23), "f16": (0x0001, 0x211F)}
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("wide,split", [(1, 2), (1, 1), (0, 1)])
+def test_qmm_mixed_fast_and_slow_tiles(device, library, oracle, monkeypatch, dtype, wide, split):
+    monkeypatch.setenv("CPQ_QMM_WIDE", str(wide))
+    monkeypatch.setenv("CPQ_QMM_SPLIT", str(split))
+    m, n, k, gs = 160, 384, 2048, 64
+    rng = np.random.default_rng(5)
+    w_q, s, b = make_weight(rng, n, k, gs, 4, dtype)
+    s[130, 3], b[130, 3] = _SLOW_SB[dtype]
+    s[300, k // gs - 1], b[300, k // gs - 1] = _SLOW_SB[dtype]
+    x = make_x(rng, m, k, dtype)
+    y = run_qmm(device, library, w_q, s, b, x, m, n, k, gs, 4, dtype)
+    ref = oracle.qmm_ref(x, w_q, s, b, m, n, k, gs, 4, dtype)
+    assert_tol(oracle, y, ref, x, k, dtype, f"mixed wide={wide} split={split}")
+
+
+def test_qmm_wide_split_is_deterministic(device, library, oracle, monkeypatch):
+    """The split-K sum adds the parts in k order whatever order the
+    workgroups finish in: repeated calls give identical bits."""
+    monkeypatch.setenv("CPQ_QMM_SPLIT", "4")
+    m, n, k, gs = 512, 1024, 4096, 64
+    rng = np.random.default_rng(9)
+    w_q, s, b = make_weight(rng, n, k, gs, 4, "bf16")
+    x = make_x(rng, m, k, "bf16")
+    W, S, B = _upload_weight(device, w_q, s, b, "bf16")
+    X = device.upload(x.reshape(-1), "bf16")
+    outs = []
+    cmds = device.commands()
+    for _ in range(3):
+        Y = device.alloc_buffer(m * n, "bf16")
+        kqmm.affine_qmm_t(cmds, library, W, S, B, X, Y, m, n, k, gs, 4)
+        cmds.commit_and_wait()
+        outs.append(Y.to_numpy())
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    ref = oracle.qmm_ref(x, w_q, s, b, m, n, k, gs, 4, "bf16")
+    assert_tol(oracle, outs[0].reshape(m, n), ref, x, k, "bf16", "wide split=4")
+
+
 def test_qmm_rejects_unaligned_n(device, library):
     W = device.alloc_buffer(40 * 128 // 8, "u32")
     S = device.alloc_buffer(40 * 2, "bf16")
