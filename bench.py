@@ -241,7 +241,7 @@ def bench_configs(dev, lib, args, rng):
                          "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
                          "hbm_frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                          "TFLOP/s": round(tf, 2), "mfma_frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 5),
-                         "kernel": "qmv" if m == 1 else ("small-M" if m <= 32 else "prefill")})
+                         "kernel": "qmv" if m == 1 else ("small-M" if m <= (64 if n <= 8192 else 32) else "prefill")})
         del cps
     res["cfg4"] = rows
 

@@ -6,6 +6,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <cstdlib>
 #include <string>
 #include <vector>
 
@@ -116,5 +117,11 @@ hipError_t launch_gather_qmm(hipStream_t s, const QuantArgs& q, const void* x, i
 
 // Row-count threshold below which cpq_quantized_matmul uses the skinny kernel.
 int skinny_max_m(const QuantArgs& q, int n, int k);
+
+// Integer from the environment (tuning and test hooks), dflt when unset.
+inline int env_int(const char* name, int dflt) {
+  const char* e = std::getenv(name);
+  return e && *e ? std::atoi(e) : dflt;
+}
 
 }  // namespace cpq

@@ -816,17 +816,8 @@ hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, i
 
 }  // namespace
 
-namespace {
-
 // CPQ_QMM_WIDE=0 turns the wide-tile kernel off; CPQ_QMM_SPLIT=1|2|4 forces
 // its K split.  Both are read per call (test and tuning hooks).
-int env_int(const char* name, int dflt) {
-  const char* e = std::getenv(name);
-  return e && *e ? std::atoi(e) : dflt;
-}
-
-}  // namespace
-
 hipError_t launch_qmm(cpq_commands* cmds, const QuantArgs& q, const void* x, void* y, int m, int n,
                       int k) {
   hipStream_t s = cmds->stream;

@@ -31,13 +31,14 @@ namespace {
 
 using namespace dev;
 
-constexpr int kWaves = 4;
 constexpr int kMaxMB = 4;  // up to 64 activation rows per pass
 
+// WAVES waves split K; MBS row blocks of 16 activation rows per pass.
+template <int WAVES, int MBS>
 struct TileShared {
-  const uint16_t* xrow[16 * kMaxMB];  // activation row per local row (nullptr: zero row)
-  uint16_t* yrow[16 * kMaxMB];        // output row per local row (nullptr: not stored)
-  float red[kWaves][kMaxMB][64][4];   // K-partial tiles
+  const uint16_t* xrow[16 * MBS];  // activation row per local row (nullptr: zero row)
+  uint16_t* yrow[16 * MBS];        // output row per local row (nullptr: not stored)
+  float red[WAVES][MBS][64][4];    // K-partial tiles
   int rows[16 * kMaxMB];              // gather: global row ids of this pass
   int count;
   int pos;
@@ -54,6 +55,7 @@ struct SlabConsts {
   u32x4 sv[kConstSlots], bv[kConstSlots];
 };
 
+template <int NT>
 __device__ __forceinline__ void slab_consts_load(const uint16_t* __restrict__ scales,
                                                  const uint16_t* __restrict__ biases, int n, int G,
                                                  int n0, bool vec, SlabConsts& sc) {
@@ -61,7 +63,7 @@ __device__ __forceinline__ void slab_consts_load(const uint16_t* __restrict__ sc
 #pragma unroll
   for (int t = 0; t < kConstSlots; ++t) {
     sc.sv[t] = sc.bv[t] = u32x4{0u, 0u, 0u, 0u};
-    const int i = threadIdx.x + 256 * t;
+    const int i = threadIdx.x + NT * t;
     if (vec && i < 16 * segs) {
       const int c = i / segs, sg = i - c * segs;
       if (n0 + c < n) {
@@ -72,7 +74,7 @@ __device__ __forceinline__ void slab_consts_load(const uint16_t* __restrict__ sc
   }
 }
 
-template <typename TT>
+template <typename TT, int NT>
 __device__ __forceinline__ bool slab_consts_store(const uint16_t* __restrict__ scales,
                                                   const uint16_t* __restrict__ biases, int n, int G,
                                                   int n0, bool vec, const SlabConsts& sc, f32x4* gc,
@@ -87,7 +89,7 @@ __device__ __forceinline__ bool slab_consts_store(const uint16_t* __restrict__ s
     const int segs = G >> 3;
 #pragma unroll
     for (int t = 0; t < kConstSlots; ++t) {
-      const int i = threadIdx.x + 256 * t;
+      const int i = threadIdx.x + NT * t;
       if (i < 16 * segs) {
         const int c = i / segs, sg = i - c * segs;
 #pragma unroll
@@ -96,7 +98,7 @@ __device__ __forceinline__ bool slab_consts_store(const uint16_t* __restrict__ s
               (h & 1) ? sc.bv[t][h >> 1] >> 16 : sc.bv[t][h >> 1] & 0xffffu);
       }
     }
-    for (int i = threadIdx.x + 256 * kConstSlots; i < 16 * segs; i += 256) {
+    for (int i = threadIdx.x + NT * kConstSlots; i < 16 * segs; i += NT) {
       const int c = i / segs, sg = i - c * segs;
       u32x4 s4 = {0u, 0u, 0u, 0u}, b4 = {0u, 0u, 0u, 0u};
       if (n0 + c < n) {
@@ -109,7 +111,7 @@ __device__ __forceinline__ bool slab_consts_store(const uint16_t* __restrict__ s
             (h & 1) ? b4[h >> 1] >> 16 : b4[h >> 1] & 0xffffu);
     }
   } else {
-    for (int it = threadIdx.x; it < 16 * G; it += 256) {
+    for (int it = threadIdx.x; it < 16 * G; it += NT) {
       const int c = it / G, gi = it - c * G;
       uint32_t sv = 0u, bv = 0u;
       if (n0 + c < n) {
@@ -128,7 +130,7 @@ __device__ __forceinline__ bool slab_consts_store(const uint16_t* __restrict__ s
 // (natural k order) and multiplied.  Steps past the wave's range read clamped
 // addresses and use zero constants (exact zero weights).  The slab constants
 // are loaded first, the weight prefetch issued behind them, and only then
-// staged to LDS.  All 256 threads must call it (contains barriers).
+// staged to LDS.  All 64 * WAVES threads must call it (contains barriers).
 template <int BITS, int MB>
 struct SkinnyGeom {
   const uint32_t* wrow;
@@ -181,11 +183,11 @@ __device__ __forceinline__ void skinny_stream(const SkinnyGeom<BITS, MB>& sg, ui
   }
 }
 
-template <typename TT, int BITS, int MB>
+template <typename TT, int BITS, int MB, int WAVES, class SH>
 __device__ __forceinline__ void skinny_tile(const uint32_t* __restrict__ w,
                                             const uint16_t* __restrict__ scales,
                                             const uint16_t* __restrict__ biases, int n, int k,
-                                            int gs_shift, int n0, f32x4* gc, TileShared& sh) {
+                                            int gs_shift, int n0, f32x4* gc, SH& sh) {
   constexpr int PF = 4;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -199,7 +201,7 @@ __device__ __forceinline__ void skinny_tile(const uint32_t* __restrict__ w,
   sg.col_ok = col < n;
   sg.chunks = k >> 5;
   const int units = (sg.chunks + 3) >> 2;
-  const int per = (units + kWaves - 1) / kWaves;
+  const int per = (units + WAVES - 1) / WAVES;
   sg.u0 = wave * per;
   sg.nu = min(units, sg.u0 + per) - sg.u0;
   sg.nsteps = (max(sg.nu, 0) + PF - 1) / PF * PF;
@@ -212,7 +214,7 @@ __device__ __forceinline__ void skinny_tile(const uint32_t* __restrict__ w,
 
   // 1. Constants' loads, then the weight / activation prefetch behind them.
   SlabConsts sc;
-  slab_consts_load(scales, biases, n, G, n0, vec, sc);
+  slab_consts_load<64 * WAVES>(scales, biases, n, G, n0, vec, sc);
   uint32_t wbuf[PF][BITS];
   u32x4 xa[2][MB][4];
   if (sg.nsteps > 0) {
@@ -221,7 +223,7 @@ __device__ __forceinline__ void skinny_tile(const uint32_t* __restrict__ w,
     sg.load_x(0, xa[0]);
   }
   // 2. Constants into LDS, vote.
-  const bool fast = slab_consts_store<TT>(scales, biases, n, G, n0, vec, sc, gc, GP);
+  const bool fast = slab_consts_store<TT, 64 * WAVES>(scales, biases, n, G, n0, vec, sc, gc, GP);
 
   // 3. Stream.
   f32x4 acc[MB];
@@ -246,11 +248,12 @@ __device__ __forceinline__ void skinny_tile(const uint32_t* __restrict__ w,
   }
   __syncthreads();
   // Each wave finishes MB/4 (at least one) of the 16-row blocks.
-  for (int mb = wave; mb < MB; mb += kWaves) {
+  for (int mb = wave; mb < MB; mb += WAVES) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float v = sh.red[0][mb][lane][i] + sh.red[1][mb][lane][i] + sh.red[2][mb][lane][i] +
-                sh.red[3][mb][lane][i];
+      float v = sh.red[0][mb][lane][i];
+#pragma unroll
+      for (int wv = 1; wv < WAVES; ++wv) v += sh.red[wv][mb][lane][i];
       const int m = 16 * mb + 4 * sg.g + i;  // D row of element i in this lane
       uint16_t* yr = sh.yrow[m];
       if (yr && sg.col_ok) yr[col] = TT::from_f32(v);
@@ -259,14 +262,14 @@ __device__ __forceinline__ void skinny_tile(const uint32_t* __restrict__ w,
   __syncthreads();
 }
 
-template <typename TT, int BITS, int MB>
-__global__ __launch_bounds__(256) void skinny_kernel(const uint32_t* __restrict__ w,
+template <typename TT, int BITS, int MB, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint32_t* __restrict__ w,
                                                      const uint16_t* __restrict__ scales,
                                                      const uint16_t* __restrict__ biases,
                                                      const uint16_t* __restrict__ x,
                                                      uint16_t* __restrict__ y, int m, int n, int k,
                                                      int gs_shift) {
-  __shared__ TileShared sh;
+  __shared__ TileShared<WAVES, MB> sh;
   extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
   f32x4* gc = reinterpret_cast<f32x4*>(dyn);
   const int n0 = blockIdx.x * 16;
@@ -277,7 +280,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(const uint32_t* __restrict_
     sh.yrow[threadIdx.x] = r < m ? y + (size_t)r * n : nullptr;
   }
   __syncthreads();
-  skinny_tile<TT, BITS, MB>(w, scales, biases, n, k, gs_shift, n0, gc, sh);
+  skinny_tile<TT, BITS, MB, WAVES>(w, scales, biases, n, k, gs_shift, n0, gc, sh);
 }
 
 // Routed experts: workgroup (16-column slab, expert e).  Rows routed to e are
@@ -290,7 +293,7 @@ __global__ __launch_bounds__(256) void gather_kernel(
     const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, int x_rows,
     const uint32_t* __restrict__ lhs, const uint32_t* __restrict__ rhs, int n_rows,
     uint16_t* __restrict__ y, int n, int k, int gs_shift, int sorted) {
-  __shared__ TileShared sh;
+  __shared__ TileShared<4, kMaxMB> sh;
   extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
   f32x4* gc = reinterpret_cast<f32x4*>(dyn);
   const int n0 = blockIdx.x * 16;
@@ -368,11 +371,11 @@ __global__ __launch_bounds__(256) void gather_kernel(
     __syncthreads();
     if (cnt == 0) continue;  // uniform: the scan reached hi without a match
     if (cnt <= 16) {
-      skinny_tile<TT, BITS, 1>(we, se, be, n, k, gs_shift, n0, gc, sh);
+      skinny_tile<TT, BITS, 1, 4>(we, se, be, n, k, gs_shift, n0, gc, sh);
     } else if (cnt <= 32) {
-      skinny_tile<TT, BITS, 2>(we, se, be, n, k, gs_shift, n0, gc, sh);
+      skinny_tile<TT, BITS, 2, 4>(we, se, be, n, k, gs_shift, n0, gc, sh);
     } else {
-      skinny_tile<TT, BITS, 4>(we, se, be, n, k, gs_shift, n0, gc, sh);
+      skinny_tile<TT, BITS, 4, 4>(we, se, be, n, k, gs_shift, n0, gc, sh);
     }
   }
 }
@@ -414,17 +417,23 @@ hipError_t launch_skinny_t(hipStream_t s, const QuantArgs& q, const void* x, voi
   const auto* xx = static_cast<const uint16_t*>(x);
   auto* yy = static_cast<uint16_t*>(y);
   const unsigned gx = (unsigned)((n + 15) / 16);
+  const unsigned gy = mb <= 2 ? 1u : (unsigned)((m + 63) / 64);
   const size_t lds = slab_consts_bytes(k, q.gs);
+  // Few slabs (under two per CU): 8 waves per workgroup keep two waves per
+  // SIMD streaming; otherwise 4.
+  static const int forced = env_int("CPQ_SKINNY_WAVES", 0);
+  const bool eight = forced ? forced == 8 : (size_t)gx * gy < 512;
+  auto go = [&](auto kern, int waves) {
+    hipLaunchKernelGGL(kern, dim3(gx, gy), dim3(64 * waves), lds, s, q.w, sc, bi, xx, yy, m, n, k, gs_shift);
+  };
   if (mb <= 1) {
-    hipLaunchKernelGGL((skinny_kernel<TT, BITS, 1>), dim3(gx, 1), dim3(256), lds, s, q.w, sc, bi, xx,
-                       yy, m, n, k, gs_shift);
+    if (eight) go(skinny_kernel<TT, BITS, 1, 8>, 8); else go(skinny_kernel<TT, BITS, 1, 4>, 4);
   } else if (mb <= 2) {
-    hipLaunchKernelGGL((skinny_kernel<TT, BITS, 2>), dim3(gx, 1), dim3(256), lds, s, q.w, sc, bi, xx,
-                       yy, m, n, k, gs_shift);
+    if (eight) go(skinny_kernel<TT, BITS, 2, 8>, 8); else go(skinny_kernel<TT, BITS, 2, 4>, 4);
   } else {
-    const unsigned gy = (unsigned)((m + 63) / 64);
-    hipLaunchKernelGGL((skinny_kernel<TT, BITS, 4>), dim3(gx, gy), dim3(256), lds, s, q.w, sc, bi,
-                       xx, yy, m, n, k, gs_shift);
+    // 64 activation rows: the activation slices dominate the L2 traffic and
+    // 4 waves measure faster than 8.
+    go(skinny_kernel<TT, BITS, 4, 4>, 4);
   }
   return hipGetLastError();
 }

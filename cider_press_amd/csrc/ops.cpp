@@ -24,17 +24,20 @@ bool kernel_available(cpq_dtype dtype, uint32_t group_size, uint32_t bits) {
 }
 
 // Largest M the routed op sends to the small-M kernel (one 16-column slab of W
-// per workgroup, up to 64 activation rows per pass).  CPQ_SKINNY_MAX_M
-// overrides it, read once per process.
+// per workgroup, up to 64 activation rows per pass).  Up to 32 rows it always
+// wins; at 33..64 rows it wins while the prefill kernel's 128-wide tiles leave
+// most CUs idle (N <= 8192: measured 19.7 vs 26.5 us at M = 64, N = K = 4096)
+// and loses once N fills the chip (58 vs 31 us at N = 12288).
+// CPQ_SKINNY_MAX_M overrides it, read once per process.
 int skinny_max_m(const QuantArgs& q, int n, int k) {
   (void)q;
-  (void)n;
   (void)k;
   static const int lim = [] {
     const char* e = std::getenv("CPQ_SKINNY_MAX_M");
-    return e && *e ? std::atoi(e) : 32;
+    return e && *e ? std::atoi(e) : 0;
   }();
-  return lim;
+  if (lim > 0) return lim;
+  return n <= 8192 ? 64 : 32;
 }
 
 namespace {

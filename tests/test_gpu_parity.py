@@ -242,6 +242,24 @@ def test_quantized_matmul_routes_all_m(device, library, oracle, m, bits, gs):
     assert_tol(oracle, y, ref, x, k, "bf16", f"routed m={m}")
 
 
+# The small-M kernel runs 8 waves per workgroup when there are few 16-column
+# slabs and 4 otherwise, and takes up to 64 rows while N <= 8192.
+@pytest.mark.parametrize("m,n,k,bits,gs", [
+    (5, 8192, 1024, 4, 64),     # 1 row block, 4 waves (512 slabs)
+    (20, 8192, 1024, 8, 64),    # 2 row blocks, 4 waves
+    (20, 4096, 2048, 4, 32),    # 2 row blocks, 8 waves
+    (48, 4096, 1024, 4, 64),    # 4 row blocks (M <= 64 at N <= 8192)
+    (64, 8192, 512, 4, 128),
+])
+def test_small_m_wave_counts(device, library, oracle, m, n, k, bits, gs):
+    rng = np.random.default_rng(m + n + k)
+    w_q, s, b = make_weight(rng, n, k, gs, bits, "bf16")
+    x = make_x(rng, m, k, "bf16")
+    y = run_qmm(device, library, w_q, s, b, x, m, n, k, gs, bits, "bf16", routed=True)
+    ref = oracle.qmm_ref(x, w_q, s, b, m, n, k, gs, bits, "bf16")
+    assert_tol(oracle, y, ref, x, k, "bf16", f"small-M m={m} n={n}")
+
+
 # The 4-bit prefill path runs the wide-tile kernel (128 x 128 tiles, K split
 # over 1, 2 or 4 workgroups, partial tiles summed by the last to finish);
 # CPQ_QMM_SPLIT forces the split, CPQ_QMM_WIDE=0 the earlier staged kernel.
