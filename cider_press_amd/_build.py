@@ -22,6 +22,7 @@ SOURCES = [
     "runtime.cpp",
     "ops.cpp",
     "graph.cpp",
+    "safetensors.cpp",
     "kernels/dequantize.hip",
     "kernels/qmv.hip",
     "kernels/skinny.hip",

@@ -20,6 +20,11 @@ BUFFER_TOO_LARGE = 4
 INVALID_ARGUMENT = 5
 COMMAND_BUFFER_FAILED = 6
 HIP_API = 7
+MISSING_KEY = 8
+UNSUPPORTED_DTYPE = 9
+SHAPE_MISMATCH = 10
+SAFETENSORS = 11
+JSON = 12
 
 # cpq_dtype
 DTYPES = {"f32": 0, "f16": 1, "bf16": 2}
@@ -63,6 +68,27 @@ class HipApi(Error):
     kind = "HipApi"
 
 
+# Loader errors (cider-press-models/src/error.rs:9-60).
+class MissingKey(Error):
+    kind = "MissingKey"
+
+
+class UnsupportedDtype(Error):
+    kind = "UnsupportedDtype"
+
+
+class ShapeMismatch(Error):
+    kind = "ShapeMismatch"
+
+
+class SafetensorsError(Error):
+    kind = "Safetensors"
+
+
+class JsonError(Error):
+    kind = "Json"
+
+
 _ERRORS = {
     NO_DEVICE: NoDevice,
     KERNEL_NOT_FOUND: KernelNotFound,
@@ -71,6 +97,11 @@ _ERRORS = {
     INVALID_ARGUMENT: InvalidArgument,
     COMMAND_BUFFER_FAILED: CommandBufferFailed,
     HIP_API: HipApi,
+    MISSING_KEY: MissingKey,
+    UNSUPPORTED_DTYPE: UnsupportedDtype,
+    SHAPE_MISMATCH: ShapeMismatch,
+    SAFETENSORS: SafetensorsError,
+    JSON: JsonError,
 }
 
 _c = ctypes
@@ -127,6 +158,20 @@ SIGNATURES = {
     "cpq_check_gather_args": (_st, [_int, _sz, _sz, _sz, _sz, _int, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
     "cpq_qweight_from_bytes": (_st, [_vp, _int, _sz, _sz, _sz, _u32, _u32, _vp, _sz, _vp, _sz, _vp, _sz, _pp]),
     "cpq_qweight_release": (None, [_vp]),
+    "cpq_qweight_info": (_st, [_vp, _psz, _psz, _psz, _c.POINTER(_u32), _c.POINTER(_u32), _c.POINTER(_int)]),
+    "cpq_safetensors_open": (_st, [_c.c_char_p, _pp]),
+    "cpq_safetensors_deserialize": (_st, [_vp, _sz, _pp]),
+    "cpq_safetensors_close": (None, [_vp]),
+    "cpq_safetensors_len": (_st, [_vp, _psz]),
+    "cpq_safetensors_name": (_st, [_vp, _sz, _c.POINTER(_c.c_char_p)]),
+    "cpq_safetensors_tensor": (_st, [_vp, _c.c_char_p, _c.POINTER(_c.c_char_p), _psz, _sz, _psz, _pp, _psz]),
+    "cpq_safetensors_metadata": (_st, [_vp, _c.c_char_p, _c.POINTER(_c.c_char_p)]),
+    "cpq_read_quantized_weight": (_st, [_vp, _vp, _c.c_char_p, _u32, _u32, _pp]),
+    "cpq_read_quantized_weight_k_padded": (_st, [_vp, _vp, _c.c_char_p, _u32, _u32, _sz, _pp]),
+    "cpq_pad_quantized_k": (_st, [_vp, _vp, _vp, _sz, _sz, _sz, _u32, _u32, _sz, _vp, _vp, _vp]),
+    "cpq_read_dense_tensor": (_st, [_vp, _vp, _c.c_char_p, _pp]),
+    "cpq_quantization_from_config": (_st, [_c.c_char_p, _sz, _c.POINTER(_int), _c.POINTER(_u32),
+                                           _c.POINTER(_u32)]),
     "cpq_tensor_from_host": (_st, [_vp, _int, _psz, _sz, _vp, _pp]),
     "cpq_tensor_quantized_matmul": (_st, [_vp, _vp, _int, _pp]),
     "cpq_tensor_dequantize": (_st, [_vp, _pp]),

@@ -190,6 +190,18 @@ cpq_status cpq_qweight_from_bytes(cpq_device* dev, cpq_dtype dtype, size_t n, si
   return CPQ_OK;
 }
 
+cpq_status cpq_qweight_info(const cpq_qweight* w, size_t* n, size_t* k_physical, size_t* k_logical,
+                            uint32_t* bits, uint32_t* group_size, cpq_dtype* dtype) {
+  if (!w || !w->p) return fail(CPQ_ERR_INVALID_ARGUMENT, "qweight_info: NULL weight");
+  if (n) *n = w->p->n;
+  if (k_physical) *k_physical = w->p->k_physical;
+  if (k_logical) *k_logical = w->p->k_logical;
+  if (bits) *bits = w->p->bits;
+  if (group_size) *group_size = w->p->group_size;
+  if (dtype) *dtype = w->p->dtype;
+  return CPQ_OK;
+}
+
 void cpq_qweight_release(cpq_qweight* w) { delete w; }
 
 cpq_status cpq_tensor_from_host(cpq_device* dev, cpq_dtype dtype, const size_t* dims, size_t ndim,

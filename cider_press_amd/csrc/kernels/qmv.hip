@@ -550,7 +550,9 @@ hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, i
   const size_t lds = (size_t)k * 2 + 16 * (G + 1) * 16 + 8 * 16 * 4;
   if constexpr (BITS == 4 || BITS == 8) {
     // Few row blocks (under two per CU): 8 waves per block keep two waves per SIMD.
-    const int waves = (n + 15) / 16 < 512 && lean_fits<BITS>(q, n, k, 8) ? 8 : 4;
+    static const int forced = env_int("CPQ_QMV_WAVES", 0);  // tuning hook: 4 or 8
+    const int waves = forced == 4 || forced == 8 ? (lean_fits<BITS>(q, n, k, forced) ? forced : 4)
+                      : (n + 15) / 16 < 512 && lean_fits<BITS>(q, n, k, 8) ? 8 : 4;
     if (lean_fits<BITS>(q, n, k, waves)) {
       const int sh = shift_of(q.gs);
       const size_t llds = (size_t)waves * lean_wave_lds(k / (128 * waves), sh) + (size_t)waves * 16 * 4;

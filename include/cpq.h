@@ -41,7 +41,13 @@ typedef enum cpq_status {
   CPQ_ERR_BUFFER_TOO_LARGE = 4,      /* Error::BufferTooLarge      error.rs:44-48 */
   CPQ_ERR_INVALID_ARGUMENT = 5,      /* Error::InvalidArgument     error.rs:56-61 */
   CPQ_ERR_COMMAND_BUFFER_FAILED = 6, /* Error::CommandBufferFailed error.rs:63-69 */
-  CPQ_ERR_HIP_API = 7                /* Error::AppleApi analogue   error.rs:50-54 */
+  CPQ_ERR_HIP_API = 7,               /* Error::AppleApi analogue   error.rs:50-54 */
+  /* Loader errors of the models crate (cider-press-models/src/error.rs:9-60). */
+  CPQ_ERR_MISSING_KEY = 8,           /* Error::MissingKey          error.rs:12-16 */
+  CPQ_ERR_UNSUPPORTED_DTYPE = 9,     /* Error::UnsupportedDtype    error.rs:18-24 */
+  CPQ_ERR_SHAPE_MISMATCH = 10,       /* Error::ShapeMismatch       error.rs:26-34 */
+  CPQ_ERR_SAFETENSORS = 11,          /* Error::Safetensors         error.rs:36-38 */
+  CPQ_ERR_JSON = 12                  /* Error::Json                error.rs:40-41 */
 } cpq_status;
 
 /* Activation / scale / bias / output element type (T). */
@@ -248,6 +254,66 @@ cpq_status cpq_tensor_shape(cpq_tensor* t, size_t* dims, size_t cap, size_t* ndi
 /* Host copy of an evaluated tensor (Tensor::cpu_slice). */
 cpq_status cpq_tensor_read(cpq_tensor* t, void* host, size_t byte_len);
 void cpq_tensor_release(cpq_tensor* t);
+
+/* QuantizedWeight accessors: logical / physical shape, quantization, T. */
+cpq_status cpq_qweight_info(const cpq_qweight* w, size_t* n, size_t* k_physical, size_t* k_logical,
+                            uint32_t* bits, uint32_t* group_size, cpq_dtype* dtype);
+
+/* ------------------------------------------------------------------ */
+/* On-disk format: MLX-style safetensors archives                        */
+/* (cider-press-models/src/safetensors_io.rs, qwen2/{weights,config}.rs) */
+/* ------------------------------------------------------------------ */
+
+/* safetensors::SafeTensors analogue.  open() maps the file read-only
+ * (tensor bytes are uploaded from the mapping); deserialize() copies an
+ * in-memory archive.  A malformed header, an unknown dtype, a byte size that
+ * does not match dtype x shape, or entries that do not tile the byte buffer
+ * return CPQ_ERR_SAFETENSORS. */
+typedef struct cpq_safetensors cpq_safetensors;
+cpq_status cpq_safetensors_open(const char* path, cpq_safetensors** out);
+cpq_status cpq_safetensors_deserialize(const void* bytes, size_t len, cpq_safetensors** out);
+void cpq_safetensors_close(cpq_safetensors* st);
+/* Tensor names, sorted. */
+cpq_status cpq_safetensors_len(const cpq_safetensors* st, size_t* n);
+cpq_status cpq_safetensors_name(const cpq_safetensors* st, size_t i, const char** name);
+/* SafeTensors::tensor: dtype name ("U32", "BF16", ...), shape, and a view of
+ * the bytes (valid until close).  CPQ_ERR_MISSING_KEY if absent. */
+cpq_status cpq_safetensors_tensor(const cpq_safetensors* st, const char* key, const char** dtype,
+                                  size_t* dims, size_t cap, size_t* ndim, const void** data,
+                                  size_t* nbytes);
+/* "__metadata__" string entries; CPQ_ERR_MISSING_KEY if absent. */
+cpq_status cpq_safetensors_metadata(const cpq_safetensors* st, const char* key, const char** value);
+
+/* read_quantized_weight (safetensors_io.rs:43-134): the triple
+ * {base}.weight (U32 [N, K*bits/32]), {base}.scales and {base}.biases
+ * ([N, K/group_size], BF16 -- or F16, both alike) into a QuantizedWeight of
+ * logical shape [N, K].  Checks in the reference's order: MissingKey,
+ * UnsupportedDtype, rank / packed-K / group divisibility (InvalidArgument),
+ * then ShapeMismatch of scales and biases.  The archive is checked before the
+ * device is touched. */
+cpq_status cpq_read_quantized_weight(cpq_device* dev, const cpq_safetensors* st, const char* base_name,
+                                     uint32_t bits, uint32_t group_size, cpq_qweight** out);
+/* build_padded_twin (qwen2/weights.rs:297-307): the same triple, zero-padded
+ * along K to k_pad (>= K, a multiple of group_size) with zero words, scales
+ * and biases; logical K stays K. */
+cpq_status cpq_read_quantized_weight_k_padded(cpq_device* dev, const cpq_safetensors* st,
+                                              const char* base_name, uint32_t bits,
+                                              uint32_t group_size, size_t k_pad, cpq_qweight** out);
+/* pad_quantized_k (qwen2/weights.rs:316-376) on host bytes: rows of
+ * k*bits/8 packed bytes and (k/gs) 16-bit scales/biases widened to k_pad;
+ * outputs are caller-allocated ([n * k_pad*bits/8], [n * (k_pad/gs) * 2]). */
+cpq_status cpq_pad_quantized_k(const void* weights, const void* scales, const void* biases, size_t n,
+                               size_t k, size_t k_pad, uint32_t bits, uint32_t group_size,
+                               size_t sb_elem_bytes, void* w_out, void* s_out, void* b_out);
+/* read_dense_tensor (safetensors_io.rs:25-32) for the graph's element types
+ * (BF16, F16); other dtypes return CPQ_ERR_UNSUPPORTED_DTYPE. */
+cpq_status cpq_read_dense_tensor(cpq_device* dev, const cpq_safetensors* st, const char* key,
+                                 cpq_tensor** out);
+/* The "quantization": {"group_size", "bits"} block of config.json
+ * (qwen2/config.rs:65-73).  *present = 0 when the key is absent or null;
+ * malformed JSON or wrongly typed fields return CPQ_ERR_JSON. */
+cpq_status cpq_quantization_from_config(const char* json, size_t len, int* present, uint32_t* bits,
+                                        uint32_t* group_size);
 
 #ifdef __cplusplus
 }
