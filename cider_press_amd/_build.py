@@ -24,6 +24,7 @@ SOURCES = [
     "graph.cpp",
     "safetensors.cpp",
     "kernels/dequantize.hip",
+    "kernels/embed.hip",
     "kernels/qmv.hip",
     "kernels/skinny.hip",
     "kernels/qmm.hip",

@@ -27,7 +27,7 @@ SAFETENSORS = 11
 JSON = 12
 
 # cpq_dtype
-DTYPES = {"f32": 0, "f16": 1, "bf16": 2}
+DTYPES = {"f32": 0, "f16": 1, "bf16": 2, "u32": 3}
 
 
 class Error(Exception):
@@ -155,6 +155,9 @@ SIGNATURES = {
     "cpq_check_qmv_args": (_st, [_int, _sz, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
     "cpq_check_qmm_args": (_st, [_int, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
     "cpq_check_dequantize_args": (_st, [_int, _sz, _sz, _sz, _sz, _u32, _u32]),
+    "cpq_check_embed_args": (_st, [_int, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
+    "cpq_embed_tokens": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _vp, _sz, _u32, _u32]),
+    "cpq_tensor_embed_tokens": (_st, [_vp, _vp, _pp]),
     "cpq_check_gather_args": (_st, [_int, _sz, _sz, _sz, _sz, _int, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
     "cpq_qweight_from_bytes": (_st, [_vp, _int, _sz, _sz, _sz, _u32, _u32, _vp, _sz, _vp, _sz, _vp, _sz, _pp]),
     "cpq_qweight_release": (None, [_vp]),

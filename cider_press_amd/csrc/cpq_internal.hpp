@@ -26,7 +26,8 @@ struct cpq_commands {
   cpq_device* dev = nullptr;
   hipStream_t stream = nullptr;
   bool owns_stream = false;
-  // Device-side status word: kernels that can detect bad data (gather indices)
+  // Device-side status words: kernels that can detect bad data count it
+  // here ([0] gather rows with out-of-range indices, [1] embed ids out of range)
   // add to it; cpq_commands_wait reads and clears it.
   unsigned int* status = nullptr;
   // Split-K scratch of the prefill kernel: arrival counters (zero between
@@ -53,7 +54,7 @@ namespace cpq {
 cpq_status fail(cpq_status st, const std::string& msg);
 cpq_status hip_fail(hipError_t e, const char* what);
 
-inline size_t dtype_size(cpq_dtype t) { return t == CPQ_DTYPE_F32 ? 4 : 2; }
+inline size_t dtype_size(cpq_dtype t) { return t == CPQ_DTYPE_F32 || t == CPQ_DTYPE_U32 ? 4 : 2; }
 
 bool kernel_available(cpq_dtype dtype, uint32_t group_size, uint32_t bits);
 
@@ -72,6 +73,10 @@ struct QuantArgs {
 };
 
 hipError_t launch_dequantize(hipStream_t s, const QuantArgs& q, void* out, size_t n_out);
+// Rows ids[t] of a [vocab, hidden] table, dequantized into out[t, :]; ids at
+// or past vocab give zero rows and are counted in *bad.
+hipError_t launch_embed(hipStream_t s, const QuantArgs& q, const uint32_t* ids, uint32_t n_ids, uint32_t vocab,
+                        uint32_t hidden, void* out, unsigned int* bad);
 
 // Decode GEMV: y[N] = x[K] . W^T for one activation row.
 hipError_t launch_qmv(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k);

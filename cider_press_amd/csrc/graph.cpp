@@ -42,15 +42,15 @@ struct QWeight {
 };
 
 struct Node {
-  enum Kind { Leaf, QuantizedMatMul, Dequantize };
+  enum Kind { Leaf, QuantizedMatMul, Dequantize, EmbedTokens };
   Kind kind = Leaf;
   cpq_device* dev = nullptr;
   cpq_dtype dtype = CPQ_DTYPE_BF16;
   std::vector<size_t> dims;
   DevBuf data;
   bool ready = false;
-  std::shared_ptr<Node> x;       // QuantizedMatMul activation
-  std::shared_ptr<QWeight> w;    // QuantizedMatMul / Dequantize weight
+  std::shared_ptr<Node> x;       // QuantizedMatMul activation / EmbedTokens ids
+  std::shared_ptr<QWeight> w;    // QuantizedMatMul / Dequantize / EmbedTokens weight
   size_t numel() const {
     size_t e = 1;
     for (size_t d : dims) e *= d;
@@ -59,7 +59,7 @@ struct Node {
 };
 
 const char* dname(cpq_dtype t) {
-  return t == CPQ_DTYPE_BF16 ? "BF16" : t == CPQ_DTYPE_F16 ? "F16" : "F32";
+  return t == CPQ_DTYPE_BF16 ? "BF16" : t == CPQ_DTYPE_F16 ? "F16" : t == CPQ_DTYPE_U32 ? "U32" : "F32";
 }
 
 cpq_status upload_into(cpq_device* dev, DevBuf& buf, const void* host, size_t bytes) {
@@ -109,6 +109,11 @@ cpq_status encode(Node& t, cpq_commands* cmds) {
                               w.w.len / 4, w.s.ptr, w.s.len / 2, w.b.ptr, w.b.len / 2, x.data.ptr,
                               x.numel(), x.data.alloc, t.data.ptr, m, w.n, w.k_physical,
                               w.group_size, w.bits);
+  } else if (t.kind == Node::EmbedTokens) {
+    const Node& ids = *t.x;
+    st = cpq_embed_tokens(cmds, w.dtype, static_cast<const uint32_t*>(w.w.ptr), w.w.len / 4, w.s.ptr,
+                          w.s.len / 2, w.b.ptr, w.b.len / 2, static_cast<const uint32_t*>(ids.data.ptr),
+                          ids.numel(), w.n, w.k_physical, t.data.ptr, t.numel(), w.group_size, w.bits);
   } else if (t.kind == Node::Dequantize) {
     st = cpq_affine_dequantize(cmds, w.dtype, static_cast<const uint32_t*>(w.w.ptr), w.w.len / 4,
                                w.s.ptr, w.s.len / 2, w.b.ptr, w.b.len / 2, t.data.ptr, t.numel(),
@@ -208,14 +213,14 @@ cpq_status cpq_tensor_from_host(cpq_device* dev, cpq_dtype dtype, const size_t* 
                                 const void* data, cpq_tensor** out) {
   if (!dev || !out || (ndim && !dims)) return fail(CPQ_ERR_INVALID_ARGUMENT, "tensor: NULL argument");
   *out = nullptr;
-  if (dtype != CPQ_DTYPE_BF16 && dtype != CPQ_DTYPE_F16)
-    return fail(CPQ_ERR_INVALID_ARGUMENT, "tensor: dtype must be BF16 or F16");
+  if (dtype != CPQ_DTYPE_BF16 && dtype != CPQ_DTYPE_F16 && dtype != CPQ_DTYPE_U32)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "tensor: dtype must be BF16, F16 or U32");
   auto t = std::make_shared<Node>();
   t->kind = Node::Leaf;
   t->dev = dev;
   t->dtype = dtype;
   t->dims.assign(dims, dims + ndim);
-  const size_t bytes = t->numel() * 2;
+  const size_t bytes = t->numel() * cpq::dtype_size(dtype);
   if (bytes && !data) return fail(CPQ_ERR_INVALID_ARGUMENT, "tensor: NULL data");
   cpq_status st = upload_into(dev, t->data, data, bytes);
   if (st != CPQ_OK) return st;
@@ -277,6 +282,32 @@ cpq_status cpq_tensor_dequantize(cpq_qweight* w, cpq_tensor** out) {
   t->dev = q.dev;
   t->dtype = q.dtype;
   t->dims = {q.n, q.k_physical};
+  t->w = w->p;
+  *out = new cpq_tensor{t};
+  return CPQ_OK;
+}
+
+// nn.rs:123-136 (embed_tokens), with Tensor::gather's index preconditions
+// (tensor.rs:1489-1514: dense, rank-1, U32).
+cpq_status cpq_tensor_embed_tokens(cpq_tensor* ids, cpq_qweight* w, cpq_tensor** out) {
+  if (!ids || !w || !out) return fail(CPQ_ERR_INVALID_ARGUMENT, "embed_tokens: NULL argument");
+  *out = nullptr;
+  const Node& x = *ids->p;
+  const QWeight& q = *w->p;
+  if (x.dev != q.dev) return fail(CPQ_ERR_INVALID_ARGUMENT, "embed_tokens: ids and weight are on different devices");
+  if (x.dims.size() != 1)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "gather: only rank-1 indices are wired (got rank " +
+                                              std::to_string(x.dims.size()) + ")");
+  if (x.dtype != CPQ_DTYPE_U32)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, std::string("gather: indices must be U32 (got ") + dname(x.dtype) + ")");
+  if (q.k_logical != q.k_physical)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "embed_tokens: the table must not be K-padded");
+  auto t = std::make_shared<Node>();
+  t->kind = Node::EmbedTokens;
+  t->dev = q.dev;
+  t->dtype = q.dtype;
+  t->dims = {x.dims[0], q.k_physical};
+  t->x = ids->p;
   t->w = w->p;
   *out = new cpq_tensor{t};
   return CPQ_OK;

@@ -286,6 +286,39 @@ cpq_status cpq_check_gather_args(cpq_dtype dtype, size_t x_rows, size_t w_q_len,
   return CPQ_OK;
 }
 
+// nn.rs:123-136 preconditions, plus the table geometry a fused kernel needs.
+cpq_status cpq_check_embed_args(cpq_dtype dtype, size_t w_q_len, size_t scales_len, size_t biases_len,
+                                size_t n_ids, size_t vocab, size_t hidden, size_t out_len, uint32_t group_size,
+                                uint32_t bits) {
+  cpq_status st = cpq::check_dtype("embed_tokens", dtype);
+  if (st != CPQ_OK) return st;
+  st = cpq_quantization_validate(bits, group_size);
+  if (st != CPQ_OK) return st;
+  if (vocab == 0 || hidden == 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "embed_tokens: table shape must be non-empty [vocab, hidden]");
+  if (hidden % group_size != 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "embed_tokens: hidden=" + std::to_string(hidden) +
+                                              " must be a multiple of group_size=" + std::to_string(group_size));
+  size_t vh, words, groups, th;
+  if (!cpq::mul_ok(vocab, hidden, &vh)) return fail(CPQ_ERR_INVALID_ARGUMENT, "embed_tokens: vocab*hidden overflows");
+  words = vh / 32 * bits;  // hidden % 32 == 0 (group sizes are >= 32)
+  groups = vh / group_size;
+  if (w_q_len != words)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "embed_tokens: w_q.len()=" + std::to_string(w_q_len) + " != vocab*hidden*bits/32 (" +
+                                              std::to_string(words) + ")");
+  if (scales_len != groups || biases_len != groups)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "embed_tokens: scales/biases length mismatch (expected " +
+                                              std::to_string(groups) + ", got scales=" + std::to_string(scales_len) +
+                                              ", biases=" + std::to_string(biases_len) + ")");
+  if (!cpq::mul_ok(n_ids, hidden, &th) || out_len != th)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "embed_tokens: out.len()=" + std::to_string(out_len) +
+                                              " != n_ids*hidden (" + std::to_string(n_ids * hidden) + ")");
+  if (vocab > 0xFFFFFFFFull || th / 32 >= (1ull << 31))
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "embed_tokens: vocab or n_ids*hidden/32 beyond 32-bit indexing");
+  if (!cpq::kernel_available(dtype, group_size, bits)) return cpq::not_found("dequantize", dtype, group_size, bits);
+  return CPQ_OK;
+}
+
 // ---------------------------------------------------------------------------
 // Ops
 // ---------------------------------------------------------------------------
@@ -336,6 +369,25 @@ cpq_status cpq_affine_dequantize(cpq_commands* cmds, cpq_dtype dtype, const uint
   cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
   return cpq::launched(cpq::launch_dequantize(cmds->stream, q, out, out_len),
                        "affine_dequantize launch");
+}
+
+cpq_status cpq_embed_tokens(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q, size_t w_q_len,
+                            const void* scales, size_t scales_len, const void* biases, size_t biases_len,
+                            const uint32_t* ids, size_t n_ids, size_t vocab, size_t hidden, void* out,
+                            size_t out_len, uint32_t group_size, uint32_t bits) {
+  if (!cmds) return fail(CPQ_ERR_INVALID_ARGUMENT, "embed_tokens: NULL command session");
+  cpq_status st = cpq_check_embed_args(dtype, w_q_len, scales_len, biases_len, n_ids, vocab, hidden, out_len,
+                                       group_size, bits);
+  if (st != CPQ_OK) return st;
+  if (n_ids == 0) return CPQ_OK;
+  st = cpq::check_ptrs("embed_tokens", w_q, scales, biases, out, out);
+  if (st != CPQ_OK) return st;
+  if (!ids || (reinterpret_cast<uintptr_t>(ids) & 3u))
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "embed_tokens: ids must be a non-NULL, 4-byte aligned device pointer");
+  cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
+  return cpq::launched(cpq::launch_embed(cmds->stream, q, ids, (uint32_t)n_ids, (uint32_t)vocab, (uint32_t)hidden,
+                                         out, cmds->status + 1),
+                       "embed_tokens launch");
 }
 
 cpq_status cpq_affine_gather_qmm(cpq_commands* cmds, cpq_dtype dtype, const void* x,

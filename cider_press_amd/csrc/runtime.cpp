@@ -203,9 +203,9 @@ cpq_status cpq_write_buffer(cpq_device* dev, void* dev_ptr, const void* host, si
 static cpq_status make_commands(cpq_device* dev, hipStream_t stream, bool owns,
                                 cpq_commands** out) {
   unsigned int* status = nullptr;
-  hipError_t e = hipMalloc(&status, sizeof(unsigned int));
+  hipError_t e = hipMalloc(&status, 2 * sizeof(unsigned int));
   if (e != hipSuccess) return hip_fail(e, "hipMalloc(status word)");
-  e = hipMemset(status, 0, sizeof(unsigned int));
+  e = hipMemset(status, 0, 2 * sizeof(unsigned int));
   if (e != hipSuccess) {
     (void)hipFree(status);
     return hip_fail(e, "hipMemset(status word)");
@@ -262,15 +262,20 @@ cpq_status cpq_commands_wait(cpq_commands* cmds) {
     return fail(CPQ_ERR_COMMAND_BUFFER_FAILED,
                 std::string("GPU command stream failed: ") + hipGetErrorName(e) + " (" +
                     hipGetErrorString(e) + ")");
-  unsigned int bad = 0;
-  e = hipMemcpy(&bad, cmds->status, sizeof(bad), hipMemcpyDeviceToHost);
+  unsigned int bad[2] = {0u, 0u};
+  e = hipMemcpy(bad, cmds->status, sizeof(bad), hipMemcpyDeviceToHost);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpy(status word)");
-  if (bad) {
-    e = hipMemset(cmds->status, 0, sizeof(unsigned int));
+  if (bad[0] || bad[1]) {
+    e = hipMemset(cmds->status, 0, sizeof(bad));
     if (e != hipSuccess) return hip_fail(e, "hipMemset(status word)");
-    return fail(CPQ_ERR_INVALID_ARGUMENT,
-                "affine_gather_qmm: " + std::to_string(bad) +
-                    " row(s) carried an out-of-range lhs/rhs index; those rows were written as 0");
+    std::string msg;
+    if (bad[0])
+      msg = "affine_gather_qmm: " + std::to_string(bad[0]) +
+            " row(s) carried an out-of-range lhs/rhs index; those rows were written as 0";
+    if (bad[1])
+      msg += std::string(msg.empty() ? "" : "; ") + "embed_tokens: " + std::to_string(bad[1]) +
+             " id(s) at or past the vocabulary size; those rows were written as 0";
+    return fail(CPQ_ERR_INVALID_ARGUMENT, msg);
   }
   return CPQ_OK;
 }

@@ -6,7 +6,7 @@ crate, crates/cider-press-kernels/src/lib.rs:35-40), backed by libcpq.so.
     device.commands()              -> device.rs:319 (one in-order HIP stream)
     Commands.commit / wait         -> commands.rs:349-419
     KernelLibrary.quantized(dev)   -> library.rs:230 (kernels are compiled ahead of time)
-    kernels.{qmv,qmm,dequantize,gather}.*  -> kernels/{qmv,qmm,dequantize}.rs
+    kernels.{qmv,qmm,dequantize,gather,embed}.*  -> kernels/{qmv,qmm,dequantize}.rs, nn.rs
 
 Buffers are typed views over device memory; 16-bit float buffers hold raw
 uint16 bit patterns on the host side (numpy has no bfloat16).
@@ -228,4 +228,4 @@ def _ptr(buf) -> ctypes.c_void_p:
     return ctypes.c_void_p(None if buf is None else buf.ptr)
 
 
-from . import dequantize, gather, qmm, qmv  # noqa: E402,F401
+from . import dequantize, embed, gather, qmm, qmv  # noqa: E402,F401

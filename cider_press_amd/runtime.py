@@ -134,7 +134,8 @@ class Tensor:
 
     @staticmethod
     def from_host(device: Device, data: np.ndarray, dtype: str = "bf16") -> "Tensor":
-        a = np.ascontiguousarray(data, dtype=np.uint16)
+        """BF16 / F16 data as raw uint16 bit patterns, or "u32" token ids."""
+        a = np.ascontiguousarray(data, dtype=np.uint32 if dtype == "u32" else np.uint16)
         dims = (ctypes.c_size_t * max(1, a.ndim))(*a.shape)
         h = ctypes.c_void_p()
         _lib.check(_lib.lib().cpq_tensor_from_host(device.handle, _lib.DTYPES[dtype], dims, a.ndim,
@@ -153,6 +154,13 @@ class Tensor:
         _lib.check(_lib.lib().cpq_tensor_dequantize(weight.handle, ctypes.byref(h)))
         return Tensor(h, weight.device, weight.dtype, keep=(weight,))
 
+    @staticmethod
+    def embed_tokens(input_ids: "Tensor", weight: QuantizedWeight) -> "Tensor":
+        """embed_tokens (nn.rs:123-136) as a lazy node: rank-1 u32 ids."""
+        h = ctypes.c_void_p()
+        _lib.check(_lib.lib().cpq_tensor_embed_tokens(input_ids._h, weight.handle, ctypes.byref(h)))
+        return Tensor(h, weight.device, weight.dtype, keep=(input_ids, weight))
+
     def eval(self) -> "Tensor":
         _lib.check(self._lib.cpq_tensor_eval(self._h))
         return self
@@ -166,7 +174,7 @@ class Tensor:
     def cpu_slice(self) -> np.ndarray:
         """Host copy of the evaluated tensor as raw uint16 bit patterns, shaped."""
         shape = self.shape()
-        out = np.empty(shape, np.uint16)
+        out = np.empty(shape, np.uint32 if self.dtype == "u32" else np.uint16)
         _lib.check(self._lib.cpq_tensor_read(self._h, out.ctypes.data_as(ctypes.c_void_p), out.nbytes))
         return out
 

@@ -54,7 +54,8 @@ typedef enum cpq_status {
 typedef enum cpq_dtype {
   CPQ_DTYPE_F32 = 0, /* accepted by validators; no f32 kernels are built */
   CPQ_DTYPE_F16 = 1,
-  CPQ_DTYPE_BF16 = 2
+  CPQ_DTYPE_BF16 = 2,
+  CPQ_DTYPE_U32 = 3  /* index tensors of the runtime graph (token ids); never a T */
 } cpq_dtype;
 
 typedef struct cpq_device cpq_device;
@@ -218,10 +219,26 @@ cpq_status cpq_check_qmm_args(cpq_dtype dtype, size_t w_q_len, size_t scales_len
 cpq_status cpq_check_dequantize_args(cpq_dtype dtype, size_t w_q_len, size_t scales_len,
                                      size_t biases_len, size_t out_len, uint32_t group_size,
                                      uint32_t bits);
+cpq_status cpq_check_embed_args(cpq_dtype dtype, size_t w_q_len, size_t scales_len, size_t biases_len,
+                                size_t n_ids, size_t vocab, size_t hidden, size_t out_len,
+                                uint32_t group_size, uint32_t bits);
 cpq_status cpq_check_gather_args(cpq_dtype dtype, size_t x_rows, size_t w_q_len,
                                  size_t scales_len, size_t biases_len, int has_lhs,
                                  size_t n_rows, size_t y_len, size_t n_experts, size_t n,
                                  size_t k, uint32_t group_size, uint32_t bits);
+
+/* embed_tokens (cider-press-models/src/nn.rs:123-136): out[t, :] =
+ * dequantize(W[ids[t], :]) for a quantized [vocab, hidden] table, T out.
+ * The reference gathers the packed words, scales and biases
+ * (Tensor::gather, runtime/src/tensor.rs:1444-1530) and dequantizes the
+ * gathered triple; here one kernel does both, bit-identical to that.
+ * ids (device, U32, n_ids) at or past vocab give zero rows and are reported
+ * by the next cpq_commands_wait as CPQ_ERR_INVALID_ARGUMENT. */
+cpq_status cpq_embed_tokens(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q, size_t w_q_len,
+                            const void* scales, size_t scales_len, const void* biases,
+                            size_t biases_len, const uint32_t* ids, size_t n_ids, size_t vocab,
+                            size_t hidden, void* out, size_t out_len, uint32_t group_size,
+                            uint32_t bits);
 
 /* ------------------------------------------------------------------ */
 /* Runtime node (runtime/src/{quantized,tensor,eval}.rs)                 */
@@ -237,7 +254,8 @@ cpq_status cpq_qweight_from_bytes(cpq_device* dev, cpq_dtype dtype, size_t n,
                                   size_t biases_bytes, cpq_qweight** out);
 void cpq_qweight_release(cpq_qweight* w);
 
-/* A dense leaf tensor uploaded from host memory (contiguous, row-major). */
+/* A dense leaf tensor uploaded from host memory (contiguous, row-major):
+ * BF16 / F16 activations, or U32 token ids. */
 cpq_status cpq_tensor_from_host(cpq_device* dev, cpq_dtype dtype, const size_t* dims,
                                 size_t ndim, const void* data, cpq_tensor** out);
 /* Tensor::quantized_matmul (tensor.rs:2064-2171): records a lazy
@@ -247,6 +265,10 @@ cpq_status cpq_tensor_quantized_matmul(cpq_tensor* x, cpq_qweight* w, int transp
 /* Tensor::dequantize_affine (tensor.rs:1558-1637): lazy Dequantize node producing
  * the dense [n, k_physical] weight. */
 cpq_status cpq_tensor_dequantize(cpq_qweight* w, cpq_tensor** out);
+/* embed_tokens (nn.rs:123-136) as a lazy node: rank-1 U32 ids against an
+ * unpadded [vocab, hidden] weight; the result is [n_ids, hidden] of the
+ * weight's T. */
+cpq_status cpq_tensor_embed_tokens(cpq_tensor* ids, cpq_qweight* w, cpq_tensor** out);
 /* Tensor::eval (tensor.rs:2681): encodes every pending node on the device's
  * session, commits and waits. */
 cpq_status cpq_tensor_eval(cpq_tensor* t);
