@@ -30,6 +30,7 @@ SOURCES = [
     "kernels/qmm.hip",
     "kernels/qmm_wide.hip",
     "kernels/gather.hip",
+    "kernels/moe.hip",
 ]
 
 ARCH = "gfx950"

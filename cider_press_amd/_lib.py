@@ -158,6 +158,8 @@ SIGNATURES = {
     "cpq_check_embed_args": (_st, [_int, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
     "cpq_embed_tokens": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _vp, _sz, _u32, _u32]),
     "cpq_tensor_embed_tokens": (_st, [_vp, _vp, _pp]),
+    "cpq_moe_route": (_st, [_vp, _int, _vp, _sz, _sz, _u32, _int, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "cpq_moe_combine": (_st, [_vp, _int, _vp, _sz, _vp, _vp, _sz, _u32, _sz, _vp, _sz]),
     "cpq_check_gather_args": (_st, [_int, _sz, _sz, _sz, _sz, _int, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
     "cpq_qweight_from_bytes": (_st, [_vp, _int, _sz, _sz, _sz, _u32, _u32, _vp, _sz, _vp, _sz, _vp, _sz, _pp]),
     "cpq_qweight_release": (None, [_vp]),

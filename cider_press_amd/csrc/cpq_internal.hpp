@@ -27,7 +27,8 @@ struct cpq_commands {
   hipStream_t stream = nullptr;
   bool owns_stream = false;
   // Device-side status words: kernels that can detect bad data count it
-  // here ([0] gather rows with out-of-range indices, [1] embed ids out of range)
+  // here ([0] gather rows with out-of-range indices, [1] embed ids out of
+  // range, [2] MoE combine positions out of range)
   // add to it; cpq_commands_wait reads and clears it.
   unsigned int* status = nullptr;
   // Split-K scratch of the prefill kernel: arrival counters (zero between
@@ -73,6 +74,16 @@ struct QuantArgs {
 };
 
 hipError_t launch_dequantize(hipStream_t s, const QuantArgs& q, void* out, size_t n_out);
+// Routed-expert plumbing (kernels/moe.hip): top-k routing, stable sort of
+// (token, slot) rows by expert, weighted combine back to tokens.
+size_t moe_sort_scratch_bytes(int rows, int n_experts);
+hipError_t launch_moe_route(hipStream_t s, int logits_dtype, const void* logits, int tokens, int n_experts, int top_k,
+                            int normalize, uint32_t* experts, float* scores);
+hipError_t launch_moe_sort(hipStream_t s, const uint32_t* experts, int rows, int top_k, int n_experts,
+                           uint32_t* scratch, uint32_t* lhs, uint32_t* rhs, uint32_t* inv, uint32_t* offsets);
+hipError_t launch_moe_combine(hipStream_t s, int dtype, const void* y, const float* scores, const uint32_t* inv,
+                              int tokens, int top_k, int n, void* out, unsigned int* bad);
+
 // Rows ids[t] of a [vocab, hidden] table, dequantized into out[t, :]; ids at
 // or past vocab give zero rows and are counted in *bad.
 hipError_t launch_embed(hipStream_t s, const QuantArgs& q, const uint32_t* ids, uint32_t n_ids, uint32_t vocab,

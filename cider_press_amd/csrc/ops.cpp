@@ -390,6 +390,63 @@ cpq_status cpq_embed_tokens(cpq_commands* cmds, cpq_dtype dtype, const uint32_t*
                        "embed_tokens launch");
 }
 
+// Routed-expert plumbing (no reference counterpart: feed-forward.md:98-107
+// names the router, top-k and gather_qmm feed as unbuilt).
+cpq_status cpq_moe_route(cpq_commands* cmds, cpq_dtype logits_dtype, const void* logits, size_t tokens,
+                         size_t n_experts, uint32_t top_k, int normalize, uint32_t* experts, float* scores,
+                         uint32_t* lhs, uint32_t* rhs, uint32_t* inv, uint32_t* offsets) {
+  if (!cmds) return fail(CPQ_ERR_INVALID_ARGUMENT, "moe_route: NULL command session");
+  cpq_status st = cpq::check_dtype("moe_route", logits_dtype);
+  if (st != CPQ_OK) return st;
+  if (n_experts == 0 || n_experts > 1024)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "moe_route: n_experts=" + std::to_string(n_experts) + " outside 1..=1024");
+  if (top_k == 0 || top_k > 16 || top_k > n_experts)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "moe_route: top_k=" + std::to_string(top_k) +
+                                              " outside 1..=min(16, n_experts)");
+  size_t rows;
+  if (!cpq::mul_ok(tokens, top_k, &rows) || rows >= (1ull << 31) || tokens * n_experts / n_experts != tokens)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "moe_route: tokens*top_k beyond 32-bit indexing");
+  if (!offsets) return fail(CPQ_ERR_INVALID_ARGUMENT, "moe_route: NULL offsets");
+  if (tokens && (!logits || !experts || !scores || !lhs || !rhs || !inv))
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "moe_route: NULL buffer");
+  void* scratch = nullptr;
+  const size_t need = cpq::kWideCounterBytes + cpq::moe_sort_scratch_bytes((int)rows, (int)n_experts);
+  hipError_t e = cpq::session_scratch(cmds, need, &scratch);
+  if (e != hipSuccess) return cpq::hip_fail(e, "moe_route: session scratch");
+  // The scratch head holds the prefill kernel's arrival counters; the sort's
+  // block histograms go after it.
+  uint32_t* hist = reinterpret_cast<uint32_t*>(static_cast<char*>(scratch) + cpq::kWideCounterBytes);
+  st = cpq::launched(cpq::launch_moe_route(cmds->stream, (int)logits_dtype, logits, (int)tokens, (int)n_experts,
+                                           (int)top_k, normalize, experts, scores),
+                     "moe_route launch");
+  if (st != CPQ_OK) return st;
+  return cpq::launched(cpq::launch_moe_sort(cmds->stream, experts, (int)rows, (int)top_k, (int)n_experts, hist, lhs,
+                                            rhs, inv, offsets),
+                       "moe_route sort launch");
+}
+
+cpq_status cpq_moe_combine(cpq_commands* cmds, cpq_dtype dtype, const void* y, size_t y_len, const float* scores,
+                           const uint32_t* inv, size_t tokens, uint32_t top_k, size_t n, void* out, size_t out_len) {
+  if (!cmds) return fail(CPQ_ERR_INVALID_ARGUMENT, "moe_combine: NULL command session");
+  if (dtype != CPQ_DTYPE_BF16 && dtype != CPQ_DTYPE_F16)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "moe_combine: dtype must be BF16 or F16");
+  if (top_k == 0 || top_k > 16) return fail(CPQ_ERR_INVALID_ARGUMENT, "moe_combine: top_k outside 1..=16");
+  if (n % 8 != 0) return fail(CPQ_ERR_INVALID_ARGUMENT, "moe_combine: N must be a multiple of 8");
+  size_t rows, yl, ol;
+  if (!cpq::mul_ok(tokens, top_k, &rows) || rows >= (1ull << 31) || !cpq::mul_ok(rows, n, &yl) ||
+      !cpq::mul_ok(tokens, n, &ol))
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "moe_combine: sizes overflow");
+  if (y_len != yl) return fail(CPQ_ERR_INVALID_ARGUMENT, "moe_combine: y.len() != tokens*top_k*N");
+  if (out_len != ol) return fail(CPQ_ERR_INVALID_ARGUMENT, "moe_combine: out.len() != tokens*N");
+  if (tokens == 0 || n == 0) return CPQ_OK;
+  if (!y || !scores || !inv || !out) return fail(CPQ_ERR_INVALID_ARGUMENT, "moe_combine: NULL buffer");
+  if ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(out)) & 15u)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "moe_combine: y and out must be 16-byte aligned");
+  return cpq::launched(cpq::launch_moe_combine(cmds->stream, (int)dtype, y, scores, inv, (int)tokens, (int)top_k,
+                                               (int)n, out, cmds->status + 2),
+                       "moe_combine launch");
+}
+
 cpq_status cpq_affine_gather_qmm(cpq_commands* cmds, cpq_dtype dtype, const void* x,
                                  size_t x_rows, const uint32_t* w_q, size_t w_q_len,
                                  const void* scales, size_t scales_len, const void* biases,

@@ -203,9 +203,9 @@ cpq_status cpq_write_buffer(cpq_device* dev, void* dev_ptr, const void* host, si
 static cpq_status make_commands(cpq_device* dev, hipStream_t stream, bool owns,
                                 cpq_commands** out) {
   unsigned int* status = nullptr;
-  hipError_t e = hipMalloc(&status, 2 * sizeof(unsigned int));
+  hipError_t e = hipMalloc(&status, 3 * sizeof(unsigned int));
   if (e != hipSuccess) return hip_fail(e, "hipMalloc(status word)");
-  e = hipMemset(status, 0, 2 * sizeof(unsigned int));
+  e = hipMemset(status, 0, 3 * sizeof(unsigned int));
   if (e != hipSuccess) {
     (void)hipFree(status);
     return hip_fail(e, "hipMemset(status word)");
@@ -262,10 +262,10 @@ cpq_status cpq_commands_wait(cpq_commands* cmds) {
     return fail(CPQ_ERR_COMMAND_BUFFER_FAILED,
                 std::string("GPU command stream failed: ") + hipGetErrorName(e) + " (" +
                     hipGetErrorString(e) + ")");
-  unsigned int bad[2] = {0u, 0u};
+  unsigned int bad[3] = {0u, 0u, 0u};
   e = hipMemcpy(bad, cmds->status, sizeof(bad), hipMemcpyDeviceToHost);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpy(status word)");
-  if (bad[0] || bad[1]) {
+  if (bad[0] || bad[1] || bad[2]) {
     e = hipMemset(cmds->status, 0, sizeof(bad));
     if (e != hipSuccess) return hip_fail(e, "hipMemset(status word)");
     std::string msg;
@@ -275,6 +275,9 @@ cpq_status cpq_commands_wait(cpq_commands* cmds) {
     if (bad[1])
       msg += std::string(msg.empty() ? "" : "; ") + "embed_tokens: " + std::to_string(bad[1]) +
              " id(s) at or past the vocabulary size; those rows were written as 0";
+    if (bad[2])
+      msg += std::string(msg.empty() ? "" : "; ") + "moe_combine: " + std::to_string(bad[2]) +
+             " (token, slot) position(s) outside the expert rows; they contributed 0";
     return fail(CPQ_ERR_INVALID_ARGUMENT, msg);
   }
   return CPQ_OK;

@@ -228,4 +228,4 @@ def _ptr(buf) -> ctypes.c_void_p:
     return ctypes.c_void_p(None if buf is None else buf.ptr)
 
 
-from . import dequantize, embed, gather, qmm, qmv  # noqa: E402,F401
+from . import dequantize, embed, gather, moe, qmm, qmv  # noqa: E402,F401

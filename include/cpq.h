@@ -240,6 +240,29 @@ cpq_status cpq_embed_tokens(cpq_commands* cmds, cpq_dtype dtype, const uint32_t*
                             size_t hidden, void* out, size_t out_len, uint32_t group_size,
                             uint32_t bits);
 
+/* Routed experts around cpq_affine_gather_qmm.  No reference counterpart:
+ * the reference names the router, top-k selection and the gather_qmm feed as
+ * its unbuilt MoE feature (docs/inference/feed-forward.md:98-107, 131-137).
+ *
+ * moe_route: per token t, p = softmax(logits[t, :]) in fp32 (logits F32,
+ * F16 or BF16, [tokens, n_experts]); experts[t*k + j] / scores[t*k + j] are
+ * the k largest p in descending order (ties: lower expert first), divided by
+ * their sum when `normalize`.  Then the rows r = t*k + j are sorted by
+ * expert, stably: lhs[p] = token and rhs[p] = expert of sorted row p (the
+ * sorted-index inputs of cpq_affine_gather_qmm), inv[r] = sorted position
+ * of row r, offsets[e] = first sorted row of expert e, offsets[E] = tokens*k.
+ * n_experts <= 1024, top_k <= min(16, n_experts).  Uses session scratch. */
+cpq_status cpq_moe_route(cpq_commands* cmds, cpq_dtype logits_dtype, const void* logits, size_t tokens,
+                         size_t n_experts, uint32_t top_k, int normalize, uint32_t* experts, float* scores,
+                         uint32_t* lhs, uint32_t* rhs, uint32_t* inv, uint32_t* offsets);
+/* moe_combine: out[t, :] = RNE_T(sum_j scores[t*k + j] * y[inv[t*k + j], :]),
+ * fp32 accumulation in j order; y is the [tokens*k, N] expert output in
+ * sorted row order.  A position outside the rows contributes nothing and is
+ * reported by the next wait as CPQ_ERR_INVALID_ARGUMENT. */
+cpq_status cpq_moe_combine(cpq_commands* cmds, cpq_dtype dtype, const void* y, size_t y_len, const float* scores,
+                           const uint32_t* inv, size_t tokens, uint32_t top_k, size_t n, void* out,
+                           size_t out_len);
+
 /* ------------------------------------------------------------------ */
 /* Runtime node (runtime/src/{quantized,tensor,eval}.rs)                 */
 /* ------------------------------------------------------------------ */
