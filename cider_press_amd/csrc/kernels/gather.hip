@@ -75,24 +75,50 @@ struct GxCursor {
   }
 };
 
-template <typename TT, int BITS, int MB, bool FAST>
-__device__ __forceinline__ void gx_stream(GxCursor<BITS> ld, GxCursor<BITS> cp, int T, int units, int my_slabs,
-                                          size_t wstride, size_t gstride, int n, int chunks, int gs_shift,
-                                          int g, int nl, const unsigned char* xs, int k, const GxShared& sh,
-                                          uint16_t* __restrict__ y) {
-  auto load = [&](const GxCursor<BITS>& c, GxStep<BITS>& dst) {
-    const int ch = min(4 * c.u + g, chunks - 1);
-    load_chunk<BITS>(c.wrow, (size_t)ch, dst.w);
-    const int gi = (ch << 5) >> gs_shift;
-    dst.s = c.srow[gi];
-    dst.b = c.brow[gi];
-  };
-  GxStep<BITS> ring[GX_PF];
+template <int BITS>
+__device__ __forceinline__ void gx_load(const GxCursor<BITS>& c, GxStep<BITS>& dst, int chunks, int g,
+                                        int gs_shift) {
+  const int ch = min(4 * c.u + g, chunks - 1);
+  load_chunk<BITS>(c.wrow, (size_t)ch, dst.w);
+  const int gi = (ch << 5) >> gs_shift;
+  dst.s = c.srow[gi];
+  dst.b = c.brow[gi];
+}
+
+// The first GX_PF steps of a wave's weight stream; `ld` ends past them.
+template <int BITS>
+__device__ __forceinline__ void gx_fill(GxCursor<BITS>& ld, GxStep<BITS> (&ring)[GX_PF], int units, int my_slabs,
+                                        size_t wstride, size_t gstride, int n, int chunks, int g, int gs_shift) {
 #pragma unroll
   for (int p = 0; p < GX_PF; ++p) {
-    load(ld, ring[p]);
+    gx_load<BITS>(ld, ring[p], chunks, g, gs_shift);
     ld.next(units, my_slabs, wstride, gstride, n);
   }
+}
+
+// First index i of the ascending a[0, n) with a[i] >= key (n if none), by one
+// wave: each round splits the candidate range into 64 sub-ranges and counts
+// the ones that end below key (a prefix, since a ascends) -- two rounds of
+// loads for n <= 4096 instead of a serial bisection.
+__device__ __forceinline__ int wave_lower_bound(const uint32_t* __restrict__ a, int n, uint32_t key, int lane) {
+  int lo = 0, len = n;
+  while (len > 1) {  // uniform
+    const int step = (len + 63) / 64;
+    const int last = lo + (lane + 1) * step - 1;  // last element of sub-range `lane`
+    const bool below = last < lo + len && a[last] < key;
+    const int c = __popcll(__ballot(below));
+    lo += c * step;
+    len = min(step, len - c * step);
+  }
+  if (len == 1 && a[lo] < key) ++lo;
+  return lo;
+}
+
+template <typename TT, int BITS, int MB, bool FAST>
+__device__ __forceinline__ void gx_stream(GxCursor<BITS> ld, GxCursor<BITS> cp, GxStep<BITS> (&ring)[GX_PF], int T,
+                                          int units, int my_slabs, size_t wstride, size_t gstride, int n, int chunks,
+                                          int gs_shift, int g, int nl, const unsigned char* xs, int k,
+                                          const GxShared& sh, int mbl, uint16_t* __restrict__ y) {
   const int TP = (T + GX_PF - 1) / GX_PF * GX_PF;
   f32x4 acc[MB];
 #pragma unroll
@@ -102,7 +128,7 @@ __device__ __forceinline__ void gx_stream(GxCursor<BITS> ld, GxCursor<BITS> cp, 
     for (int p = 0; p < GX_PF; ++p) {
       const int t = t0 + p;
       const GxStep<BITS> cur = ring[p];
-      load(ld, ring[p]);  // clamped past the end: no branch, no wait
+      gx_load<BITS>(ld, ring[p], chunks, g, gs_shift);  // clamped past the end: no branch, no wait
       ld.next(units, my_slabs, wstride, gstride, n);
       const int c = 4 * cp.u + g;
       const bool live = t < T && c < chunks && cp.col < n;
@@ -118,6 +144,7 @@ __device__ __forceinline__ void gx_stream(GxCursor<BITS> ld, GxCursor<BITS> cp, 
       const int cq = min(c, chunks - 1) * 4;  // first 16-byte chunk of this lane's 32 k
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
+        if (mb >= mbl) break;  // 16-row blocks past the pass's rows (wave-uniform)
         const unsigned char* xr = xs + (size_t)(16 * mb + nl) * k * 2;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -129,6 +156,7 @@ __device__ __forceinline__ void gx_stream(GxCursor<BITS> ld, GxCursor<BITS> cp, 
         if (t < T && cp.col < n) {
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb) {
+            if (mb >= mbl) break;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const int rl = 16 * mb + 4 * g + i;
@@ -171,14 +199,16 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
   // 1. Rows routed to e.
   const int nblk = (n_rows + 63) >> 6;
   if (sorted) {
+    // [lo, hi) = equal range of e in the ascending rhs; waves 0 and 1 search
+    // its two ends at once.
+    if (wave < 2) {
+      const int b = wave_lower_bound(rhs, n_rows, e + (uint32_t)wave, lane);
+      if (lane == 0) sh.cnt[wave] = b;
+    }
+    __syncthreads();
     if (tid == 0) {
-      int a = 0, b = n_rows;
-      while (a < b) { const int mid = (a + b) >> 1; if (rhs[mid] < e) a = mid + 1; else b = mid; }
-      const int lo = a;
-      b = n_rows;
-      while (a < b) { const int mid = (a + b) >> 1; if (rhs[mid] <= e) a = mid + 1; else b = mid; }
-      sh.lo = lo;
-      sh.total = a - lo;
+      sh.lo = sh.cnt[0];
+      sh.total = sh.cnt[1] - sh.cnt[0];
     }
   } else {
     for (int b = wave; b < nblk; b += GX_WAVES) {
@@ -201,6 +231,25 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
   __syncthreads();
   const int total = sh.total;
   if (total == 0) return;  // uniform
+
+  // Wave w's slabs: 16-column slabs w, w+8, ... of the chunk.  Their first
+  // GX_PF weight steps are requested now, so the stream is in flight while
+  // the constants are voted on and the activations staged.
+  const int nslab = (ncols + 15) >> 4;
+  const int my_slabs = nslab > wave ? (nslab - wave + GX_WAVES - 1) / GX_WAVES : 0;
+  const int T = my_slabs * units;  // live steps of this wave
+  const size_t wstride = (size_t)16 * GX_WAVES * words_per_row, gstride = (size_t)16 * GX_WAVES * G;
+  GxCursor<BITS> start;
+  start.u = 0;
+  start.slab = 0;
+  start.col = c0 + 16 * wave + nl;
+  const int col0 = min(start.col, n - 1);
+  start.wrow = we + (size_t)col0 * words_per_row;
+  start.srow = se + (size_t)col0 * G;
+  start.brow = be + (size_t)col0 * G;
+  GxStep<BITS> ring[GX_PF];
+  GxCursor<BITS> ld = start;
+  if (T > 0) gx_fill<BITS>(ld, ring, units, my_slabs, wstride, gstride, n, chunks, g, gs_shift);
 
   // 2. Fast-path vote over the chunk's (column, group) pairs.
   bool ok = true;
@@ -233,20 +282,6 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
   }
   bool fast = __syncthreads_and(ok);
   if constexpr (BITS != 4 && BITS != 8) fast = false;
-
-  // Wave w's slabs: 16-column slabs w, w+8, ... of the chunk.
-  const int nslab = (ncols + 15) >> 4;
-  const int my_slabs = nslab > wave ? (nslab - wave + GX_WAVES - 1) / GX_WAVES : 0;
-  const int T = my_slabs * units;  // live steps of this wave
-  const size_t wstride = (size_t)16 * GX_WAVES * words_per_row, gstride = (size_t)16 * GX_WAVES * G;
-  GxCursor<BITS> start;
-  start.u = 0;
-  start.slab = 0;
-  start.col = c0 + 16 * wave + nl;
-  const int col0 = min(start.col, n - 1);
-  start.wrow = we + (size_t)col0 * words_per_row;
-  start.srow = se + (size_t)col0 * G;
-  start.brow = be + (size_t)col0 * G;
 
   for (int p0 = 0; p0 < total; p0 += R) {
     // 3. The pass's rows and activation rows.
@@ -305,14 +340,20 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
     }
     __syncthreads();
 
-    // 5. Stream the weights of this wave's slabs.
+    // 5. Stream the weights of this wave's slabs; only the 16-row blocks
+    //    that hold rows of this pass are multiplied.
+    const int mbl = (min(R, total - p0) + 15) >> 4;
     if (T > 0) {
+      if (p0 > 0) {  // a further pass streams the weights again
+        ld = start;
+        gx_fill<BITS>(ld, ring, units, my_slabs, wstride, gstride, n, chunks, g, gs_shift);
+      }
       if (fast)
-        gx_stream<TT, BITS, MB, true>(start, start, T, units, my_slabs, wstride, gstride, n, chunks, gs_shift,
-                                      g, nl, xs, k, sh, y);
+        gx_stream<TT, BITS, MB, true>(ld, start, ring, T, units, my_slabs, wstride, gstride, n, chunks, gs_shift,
+                                      g, nl, xs, k, sh, mbl, y);
       else
-        gx_stream<TT, BITS, MB, false>(start, start, T, units, my_slabs, wstride, gstride, n, chunks,
-                                       gs_shift, g, nl, xs, k, sh, y);
+        gx_stream<TT, BITS, MB, false>(ld, start, ring, T, units, my_slabs, wstride, gstride, n, chunks,
+                                       gs_shift, g, nl, xs, k, sh, mbl, y);
     }
     __syncthreads();  // LDS rows / activations are rewritten by the next pass
   }
