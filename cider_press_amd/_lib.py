@@ -155,6 +155,9 @@ SIGNATURES = {
     "cpq_check_qmv_args": (_st, [_int, _sz, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
     "cpq_check_qmm_args": (_st, [_int, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
     "cpq_check_dequantize_args": (_st, [_int, _sz, _sz, _sz, _sz, _u32, _u32]),
+    "cpq_check_qmm_n_args": (_st, [_int, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
+    "cpq_affine_qmm_n": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz,
+                               _u32, _u32]),
     "cpq_check_embed_args": (_st, [_int, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
     "cpq_embed_tokens": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _vp, _sz, _u32, _u32]),
     "cpq_tensor_embed_tokens": (_st, [_vp, _vp, _pp]),

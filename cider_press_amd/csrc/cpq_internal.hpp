@@ -74,6 +74,12 @@ struct QuantArgs {
 };
 
 hipError_t launch_dequantize(hipStream_t s, const QuantArgs& q, void* out, size_t n_out);
+// Y[M, N] = X[M, K] . dequant(W[K, N]) (MLX transpose=false); N % 32 == 0,
+// K % 8 == 0.  split > 1 splits K and needs qmm_n_scratch_bytes of fp32 partials.
+int qmm_n_split(int m, int n, int k, int cu_count);
+size_t qmm_n_scratch_bytes(int m, int n, int split);
+hipError_t launch_qmm_n(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k, int split,
+                        float* partial);
 // Routed-expert plumbing (kernels/moe.hip): top-k routing, stable sort of
 // (token, slot) rows by expert, weighted combine back to tokens.
 size_t moe_sort_scratch_bytes(int rows, int n_experts);

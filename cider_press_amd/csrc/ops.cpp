@@ -319,6 +319,36 @@ cpq_status cpq_check_embed_args(cpq_dtype dtype, size_t w_q_len, size_t scales_l
   return CPQ_OK;
 }
 
+// qmm_n / qvm (transpose=false): W is [K, N] packed along N, groups along N.
+cpq_status cpq_check_qmm_n_args(cpq_dtype dtype, size_t w_q_len, size_t scales_len, size_t biases_len,
+                                size_t x_len, size_t y_len, size_t m, size_t n, size_t k, uint32_t group_size,
+                                uint32_t bits) {
+  cpq_status st = cpq::check_dtype("affine_qmm_n", dtype);
+  if (st != CPQ_OK) return st;
+  st = cpq_quantization_validate(bits, group_size);
+  if (st != CPQ_OK) return st;
+  if (n % group_size != 0 || n % 32 != 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_n: N=" + std::to_string(n) +
+                                              " must be a multiple of 32 and of group_size=" +
+                                              std::to_string(group_size));
+  if (k % 8 != 0) return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_n: K=" + std::to_string(k) + " must be a multiple of 8");
+  size_t kn, mk, mn;
+  if (!cpq::mul_ok(k, n, &kn) || !cpq::mul_ok(m, k, &mk) || !cpq::mul_ok(m, n, &mn))
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_n: sizes overflow usize");
+  if (w_q_len != kn / 32 * bits)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_n: w_q.len()=" + std::to_string(w_q_len) + " != K*N*bits/32 (" +
+                                              std::to_string(kn / 32 * bits) + ")");
+  if (scales_len != kn / group_size || biases_len != kn / group_size)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_n: scales/biases length mismatch (expected " +
+                                              std::to_string(kn / group_size) + ")");
+  if (x_len != mk) return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_n: x.len() != M*K");
+  if (y_len != mn) return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_n: y.len() != M*N");
+  if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_n: dimensions beyond 32-bit indexing");
+  if (!cpq::kernel_available(dtype, group_size, bits)) return cpq::not_found("qmm_n", dtype, group_size, bits);
+  return CPQ_OK;
+}
+
 // ---------------------------------------------------------------------------
 // Ops
 // ---------------------------------------------------------------------------
@@ -369,6 +399,35 @@ cpq_status cpq_affine_dequantize(cpq_commands* cmds, cpq_dtype dtype, const uint
   cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
   return cpq::launched(cpq::launch_dequantize(cmds->stream, q, out, out_len),
                        "affine_dequantize launch");
+}
+
+cpq_status cpq_affine_qmm_n(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q, size_t w_q_len,
+                            const void* scales, size_t scales_len, const void* biases, size_t biases_len,
+                            const void* x, size_t x_len, void* y, size_t y_len, size_t m, size_t n, size_t k,
+                            uint32_t group_size, uint32_t bits) {
+  if (!cmds) return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_n: NULL command session");
+  cpq_status st = cpq_check_qmm_n_args(dtype, w_q_len, scales_len, biases_len, x_len, y_len, m, n, k, group_size,
+                                       bits);
+  if (st != CPQ_OK) return st;
+  if (m == 0 || n == 0) return CPQ_OK;
+  st = cpq::check_ptrs("affine_qmm_n", k ? w_q : reinterpret_cast<const uint32_t*>(y), k ? scales : y,
+                       k ? biases : y, k ? x : y, y);
+  if (st != CPQ_OK) return st;
+  cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
+  // Few output tiles: split K into fp32 partials in session scratch (past the
+  // prefill kernel's counters); without scratch (graph capture), no split.
+  int split = cpq::qmm_n_split((int)m, (int)n, (int)k, cmds->dev ? cmds->dev->cu_count : 0);
+  float* partial = nullptr;
+  if (split > 1) {
+    void* scratch = nullptr;
+    if (cpq::session_scratch(cmds, cpq::kWideCounterBytes + cpq::qmm_n_scratch_bytes((int)m, (int)n, split),
+                             &scratch) == hipSuccess)
+      partial = reinterpret_cast<float*>(static_cast<char*>(scratch) + cpq::kWideCounterBytes);
+    else
+      split = 1;
+  }
+  return cpq::launched(cpq::launch_qmm_n(cmds->stream, q, x, y, (int)m, (int)n, (int)k, split, partial),
+                       "affine_qmm_n launch");
 }
 
 cpq_status cpq_embed_tokens(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q, size_t w_q_len,

@@ -29,3 +29,19 @@ def quantized_matmul(commands: Commands, w_q: Buffer, scales: Buffer, biases: Bu
         commands.handle, _lib.DTYPES[scales.dtype], _ptr(w_q), len(w_q), _ptr(scales), len(scales),
         _ptr(biases), len(biases), _ptr(x), len(x) if x_len is None else x_len, x.alloc_len, _ptr(y),
         m, n, k_physical, group_size, bits))
+
+
+def affine_qmm_n(commands: Commands, library: KernelLibrary, w_q: Buffer, scales: Buffer, biases: Buffer,
+                 x: Buffer, y: Buffer, m: int, n: int, k: int, group_size: int, bits: int) -> None:
+    """MLX transpose=false (quantized.h:1215-1349): Y[M,N] = X[M,K] . dequant(W) with
+    W logically [K, N] (w_q [K, N*bits/32], scales/biases [K, N/gs]). Encodes only."""
+    del library
+    _lib.check(_lib.lib().cpq_affine_qmm_n(
+        commands.handle, _lib.DTYPES[scales.dtype], _ptr(w_q), len(w_q), _ptr(scales), len(scales),
+        _ptr(biases), len(biases), _ptr(x), len(x), _ptr(y), len(y), m, n, k, group_size, bits))
+
+
+def affine_qvm(commands: Commands, library: KernelLibrary, w_q: Buffer, scales: Buffer, biases: Buffer,
+               x: Buffer, y: Buffer, in_vec_size: int, out_vec_size: int, group_size: int, bits: int) -> None:
+    """MLX affine_qvm (quantized.h:977-1086): y = x . dequant(W), W [in_vec_size, out_vec_size]."""
+    affine_qmm_n(commands, library, w_q, scales, biases, x, y, 1, out_vec_size, in_vec_size, group_size, bits)

@@ -227,6 +227,21 @@ cpq_status cpq_check_gather_args(cpq_dtype dtype, size_t x_rows, size_t w_q_len,
                                  size_t n_rows, size_t y_len, size_t n_experts, size_t n,
                                  size_t k, uint32_t group_size, uint32_t bits);
 
+/* affine_qmm_n / affine_qvm (MLX transpose=false; quantized.h:977-1086,
+ * 1215-1349): Y[M, N] = X[M, K] . dequant(W) with W logically [K, N] --
+ * w_q [K, N*bits/32] packed along N, scales / biases [K, N/group_size].
+ * qvm is the M == 1 case.  Same numerics contract as cpq_affine_qmm_t.
+ * N % 32 == 0 and K % 8 == 0.  The reference's runtime rejects
+ * transpose=false (tensor.rs:2069-2075), so cpq_quantized_matmul and the
+ * graph node do too; this is the kernels-level op. */
+cpq_status cpq_check_qmm_n_args(cpq_dtype dtype, size_t w_q_len, size_t scales_len, size_t biases_len,
+                                size_t x_len, size_t y_len, size_t m, size_t n, size_t k,
+                                uint32_t group_size, uint32_t bits);
+cpq_status cpq_affine_qmm_n(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q, size_t w_q_len,
+                            const void* scales, size_t scales_len, const void* biases, size_t biases_len,
+                            const void* x, size_t x_len, void* y, size_t y_len, size_t m, size_t n, size_t k,
+                            uint32_t group_size, uint32_t bits);
+
 /* embed_tokens (cider-press-models/src/nn.rs:123-136): out[t, :] =
  * dequantize(W[ids[t], :]) for a quantized [vocab, hidden] table, T out.
  * The reference gathers the packed words, scales and biases
