@@ -155,6 +155,10 @@ SIGNATURES = {
     "cpq_check_qmv_args": (_st, [_int, _sz, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
     "cpq_check_qmm_args": (_st, [_int, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
     "cpq_check_dequantize_args": (_st, [_int, _sz, _sz, _sz, _sz, _u32, _u32]),
+    "cpq_affine_qmm_t_batched": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz,
+                                       _u32, _u32, _int, _c.POINTER(_int), _c.POINTER(_c.c_int64), _c.POINTER(_c.c_int64), _c.POINTER(_c.c_int64), _c.POINTER(_c.c_int64)]),
+    "cpq_affine_qmv_batched": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz,
+                                     _u32, _u32, _int, _c.POINTER(_int), _c.POINTER(_c.c_int64), _c.POINTER(_c.c_int64), _c.POINTER(_c.c_int64), _c.POINTER(_c.c_int64)]),
     "cpq_check_qmm_n_args": (_st, [_int, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _sz, _u32, _u32]),
     "cpq_affine_qmm_n": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz,
                                _u32, _u32]),

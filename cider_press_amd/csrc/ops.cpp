@@ -385,6 +385,136 @@ cpq_status cpq_affine_qmm_t(cpq_commands* cmds, cpq_dtype dtype, const uint32_t*
                        "affine_qmm_t launch");
 }
 
+// ---------------------------------------------------------------------------
+// Batched forms (MLX's `batched` kernels, adjust_matrix_offsets in
+// quantized.h:1351-1388): batch element z picks its x, w, scales and biases
+// through per-dimension element strides over the batch shape (stride 0
+// broadcasts); y is contiguous, one [M, N] block per element.
+// ---------------------------------------------------------------------------
+
+namespace {
+
+constexpr int kMaxBatchDims = 8;
+
+int64_t batch_offset(size_t z, int nd, const int* shape, const int64_t* st) {
+  int64_t off = 0;
+  for (int d = nd - 1; d >= 0; --d) {
+    off += (int64_t)(z % (size_t)shape[d]) * st[d];
+    z /= (size_t)shape[d];
+  }
+  return off;
+}
+
+// Element count of the batch, and every operand's batch elements inside its
+// buffer (largest offset + one matrix <= length) with offsets that keep the
+// kernels' alignment (`align` elements).
+cpq_status check_batch(const char* op, int nd, const int* shape, const int64_t* const st[4], const size_t extent[4],
+                       const size_t len[4], const size_t align[4], size_t* count) {
+  const char* names[4] = {"w_q", "scales", "biases", "x"};
+  if (nd < 0 || nd > kMaxBatchDims)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, std::string(op) + ": batch_ndims outside 0..=8");
+  if (nd && !shape) return fail(CPQ_ERR_INVALID_ARGUMENT, std::string(op) + ": NULL batch_shape");
+  size_t c = 1;
+  for (int d = 0; d < nd; ++d) {
+    if (shape[d] < 0) return fail(CPQ_ERR_INVALID_ARGUMENT, std::string(op) + ": negative batch dimension");
+    if (!cpq::mul_ok(c, (size_t)shape[d], &c))
+      return fail(CPQ_ERR_INVALID_ARGUMENT, std::string(op) + ": batch size overflows");
+  }
+  *count = c;
+  if (c == 0) return CPQ_OK;
+  for (int o = 0; o < 4; ++o) {
+    if (nd && !st[o]) return fail(CPQ_ERR_INVALID_ARGUMENT, std::string(op) + ": NULL " + names[o] + " strides");
+    int64_t mx = 0;
+    for (int d = 0; d < nd; ++d) {
+      if (st[o][d] < 0) return fail(CPQ_ERR_INVALID_ARGUMENT, std::string(op) + ": negative " + names[o] + " stride");
+      if (st[o][d] % (int64_t)align[o] != 0)
+        return fail(CPQ_ERR_INVALID_ARGUMENT, std::string(op) + ": " + names[o] + " stride " +
+                                                  std::to_string(st[o][d]) + " breaks its " +
+                                                  std::to_string(align[o]) + "-element alignment");
+      if (shape[d] > 1 && st[o][d] > (INT64_MAX - mx) / (shape[d] - 1))
+        return fail(CPQ_ERR_INVALID_ARGUMENT, std::string(op) + ": batch offsets overflow");
+      mx += (int64_t)(shape[d] - 1) * st[o][d];
+    }
+    if ((uint64_t)mx + extent[o] > len[o])
+      return fail(CPQ_ERR_INVALID_ARGUMENT, std::string(op) + ": " + names[o] + " batch elements reach past its " +
+                                                std::to_string(len[o]) + " elements");
+  }
+  return CPQ_OK;
+}
+
+}  // namespace
+
+cpq_status cpq_affine_qmm_t_batched(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q, size_t w_q_len,
+                                    const void* scales, size_t scales_len, const void* biases, size_t biases_len,
+                                    const void* x, size_t x_len, void* y, size_t y_len, size_t m, size_t n,
+                                    size_t k, uint32_t group_size, uint32_t bits, int batch_ndims,
+                                    const int* batch_shape, const int64_t* w_strides, const int64_t* s_strides,
+                                    const int64_t* b_strides, const int64_t* x_strides) {
+  if (!cmds) return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t_batched: NULL command session");
+  size_t mk, mn, nk;
+  if (!cpq::mul_ok(m, k, &mk) || !cpq::mul_ok(m, n, &mn) || !cpq::mul_ok(n, k, &nk))
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t_batched: sizes overflow usize");
+  const size_t words = nk / 32 * bits, groups = group_size ? nk / group_size : 0;
+  cpq_status st = cpq_check_qmm_args(dtype, words, groups, groups, mk, mn, m, n, k, group_size, bits);
+  if (st != CPQ_OK) return st;
+  const int64_t* strides[4] = {w_strides, s_strides, b_strides, x_strides};
+  const size_t extent[4] = {words, groups, groups, mk};
+  const size_t len[4] = {w_q_len, scales_len, biases_len, x_len};
+  const size_t align[4] = {4, 1, 1, 8};  // 16-byte weight and activation rows
+  size_t count;
+  st = check_batch("affine_qmm_t_batched", batch_ndims, batch_shape, strides, extent, len, align, &count);
+  if (st != CPQ_OK) return st;
+  size_t ylen;
+  if (!cpq::mul_ok(count, mn, &ylen) || y_len != ylen)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t_batched: y.len() != batch*M*N");
+  const size_t esz = cpq::dtype_size(dtype);
+  for (size_t z = 0; z < count; ++z) {
+    const uint32_t* wz = w_q + batch_offset(z, batch_ndims, batch_shape, w_strides);
+    const char* sz = static_cast<const char*>(scales) + batch_offset(z, batch_ndims, batch_shape, s_strides) * esz;
+    const char* bz = static_cast<const char*>(biases) + batch_offset(z, batch_ndims, batch_shape, b_strides) * esz;
+    const char* xz = static_cast<const char*>(x) + batch_offset(z, batch_ndims, batch_shape, x_strides) * esz;
+    char* yz = static_cast<char*>(y) + z * mn * esz;
+    st = cpq_affine_qmm_t(cmds, dtype, wz, words, sz, groups, bz, groups, xz, mk, yz, mn, m, n, k, group_size, bits);
+    if (st != CPQ_OK) return st;
+  }
+  return CPQ_OK;
+}
+
+cpq_status cpq_affine_qmv_batched(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q, size_t w_q_len,
+                                  const void* scales, size_t scales_len, const void* biases, size_t biases_len,
+                                  const void* x, size_t x_len, void* y, size_t y_len, size_t n, size_t k,
+                                  uint32_t group_size, uint32_t bits, int batch_ndims, const int* batch_shape,
+                                  const int64_t* w_strides, const int64_t* s_strides, const int64_t* b_strides,
+                                  const int64_t* x_strides) {
+  if (!cmds) return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmv_batched: NULL command session");
+  size_t nk;
+  if (!cpq::mul_ok(n, k, &nk)) return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmv_batched: N*K overflows usize");
+  const size_t words = nk / 32 * bits, groups = group_size ? nk / group_size : 0;
+  const size_t esz = cpq::dtype_size(dtype);
+  cpq_status st = cpq_check_qmv_args(dtype, words, groups, groups, k * esz, n, k, group_size, bits);
+  if (st != CPQ_OK) return st;
+  const int64_t* strides[4] = {w_strides, s_strides, b_strides, x_strides};
+  const size_t extent[4] = {words, groups, groups, k};
+  const size_t len[4] = {w_q_len, scales_len, biases_len, x_len};
+  const size_t align[4] = {4, 1, 1, 8};
+  size_t count;
+  st = check_batch("affine_qmv_batched", batch_ndims, batch_shape, strides, extent, len, align, &count);
+  if (st != CPQ_OK) return st;
+  size_t ylen;
+  if (!cpq::mul_ok(count, n, &ylen) || y_len != ylen)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmv_batched: y.len() != batch*N");
+  for (size_t z = 0; z < count; ++z) {
+    const uint32_t* wz = w_q + batch_offset(z, batch_ndims, batch_shape, w_strides);
+    const char* sz = static_cast<const char*>(scales) + batch_offset(z, batch_ndims, batch_shape, s_strides) * esz;
+    const char* bz = static_cast<const char*>(biases) + batch_offset(z, batch_ndims, batch_shape, b_strides) * esz;
+    const char* xz = static_cast<const char*>(x) + batch_offset(z, batch_ndims, batch_shape, x_strides) * esz;
+    char* yz = static_cast<char*>(y) + z * n * esz;
+    st = cpq_affine_qmv(cmds, dtype, wz, words, sz, groups, bz, groups, xz, k * esz, yz, n, k, group_size, bits);
+    if (st != CPQ_OK) return st;
+  }
+  return CPQ_OK;
+}
+
 cpq_status cpq_affine_dequantize(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q,
                                  size_t w_q_len, const void* scales, size_t scales_len,
                                  const void* biases, size_t biases_len, void* out,

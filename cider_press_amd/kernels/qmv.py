@@ -25,3 +25,19 @@ def affine_qmv_bf16(commands, library, w_q, scales, biases, x, y, in_vec_size, g
         if b.dtype != "bf16":
             raise TypeError("affine_qmv_bf16: scales, biases, x and y must be bf16 buffers")
     affine_qmv(commands, library, w_q, scales, biases, x, y, in_vec_size, group_size, bits)
+
+
+def affine_qmv_batched(commands: Commands, library: KernelLibrary, w_q: Buffer, scales: Buffer, biases: Buffer,
+                       x: Buffer, y: Buffer, in_vec_size: int, out_vec_size: int, group_size: int, bits: int,
+                       batch_shape, w_strides, s_strides, b_strides, x_strides) -> None:
+    """MLX's batched qmv (quantized.h:1496-1546 with batched=true): one activation
+    row per batch element, W / scales / biases / x at element strides (0
+    broadcasts); y holds out_vec_size values per element."""
+    from .qmm import _batch_args
+
+    del library
+    nd, shape, (ws, ss, bs, xs) = _batch_args(batch_shape, w_strides, s_strides, b_strides, x_strides)
+    _lib.check(_lib.lib().cpq_affine_qmv_batched(
+        commands.handle, _lib.DTYPES[scales.dtype], _ptr(w_q), len(w_q), _ptr(scales), len(scales),
+        _ptr(biases), len(biases), _ptr(x), len(x), _ptr(y), len(y), out_vec_size, in_vec_size, group_size, bits,
+        nd, shape, ws, ss, bs, xs))

@@ -227,6 +227,28 @@ cpq_status cpq_check_gather_args(cpq_dtype dtype, size_t x_rows, size_t w_q_len,
                                  size_t n_rows, size_t y_len, size_t n_experts, size_t n,
                                  size_t k, uint32_t group_size, uint32_t bits);
 
+/* Batched qmv / qmm_t (MLX's `batched` kernel variants; adjust_matrix_offsets,
+ * quantized.h:1351-1388): over batch_shape[batch_ndims] (row-major), element z
+ * takes its W, scales, biases and x at the given element strides (u32 words
+ * for w_q, T elements otherwise; stride 0 broadcasts), and writes its
+ * [M, N] (qmv: [N]) block of y contiguously at z*M*N.  Each element's matrix
+ * must lie inside its buffer; w_q strides must be multiples of 4 words and x
+ * strides of 8 elements.  Each element is one single-matrix launch on the
+ * session stream (encode only). */
+cpq_status cpq_affine_qmm_t_batched(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q, size_t w_q_len,
+                                    const void* scales, size_t scales_len, const void* biases,
+                                    size_t biases_len, const void* x, size_t x_len, void* y, size_t y_len,
+                                    size_t m, size_t n, size_t k, uint32_t group_size, uint32_t bits,
+                                    int batch_ndims, const int* batch_shape, const int64_t* w_strides,
+                                    const int64_t* s_strides, const int64_t* b_strides,
+                                    const int64_t* x_strides);
+cpq_status cpq_affine_qmv_batched(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q, size_t w_q_len,
+                                  const void* scales, size_t scales_len, const void* biases, size_t biases_len,
+                                  const void* x, size_t x_len, void* y, size_t y_len, size_t n, size_t k,
+                                  uint32_t group_size, uint32_t bits, int batch_ndims, const int* batch_shape,
+                                  const int64_t* w_strides, const int64_t* s_strides, const int64_t* b_strides,
+                                  const int64_t* x_strides);
+
 /* affine_qmm_n / affine_qvm (MLX transpose=false; quantized.h:977-1086,
  * 1215-1349): Y[M, N] = X[M, K] . dequant(W) with W logically [K, N] --
  * w_q [K, N*bits/32] packed along N, scales / biases [K, N/group_size].
