@@ -543,33 +543,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   wide_wload<0>(g, 1, wr[1]);
   __builtin_amdgcn_sched_barrier(0);
 
-  // 3. Constants into LDS: f32 b at [(group * 32 + c % 32) * 4 + c / 32]
-  //    and the raw 16-bit scale at the same index of the scale array, for
-  //    column col0 + c.  The workgroup votes on the fast dequantization, and
-  //    if it passes every thread rewrites its own b as c0 = b - 1024 s.
+  // 3. Constants into LDS: f32 c0 = b - 1024 s (fast dequantization) or b
+  //    (generic) at [(group * 32 + c % 32) * 4 + c / 32] and the raw 16-bit
+  //    scale at the same index of the scale array, for column col0 + c.
+  //    Each thread checks its groups (packed exponent check, the exact
+  //    predicate only when that one is inconclusive) and stores c0 if they
+  //    pass, b if not; the workgroup then votes, and if the vote fails the
+  //    threads that stored c0 store b instead.  With one wave per SIMD every
+  //    instruction here costs several cycles, so the common path is kept to
+  //    a few per group.
   float* cstb = reinterpret_cast<float*>(smem + cst_base);
   uint16_t* csts = reinterpret_cast<uint16_t*>(smem + cst_base + (size_t)GL * 512);
   const int cidx = (cc & 31) * 4 + (cc >> 5);
-  bool ok = true;
+  FastQuick fq;
+  fast_quick_init(fq);
 #pragma unroll
-  for (int u = 0; u < WMAXB; ++u) {
-    const int gb = half + 2 * u;
-    if (8 * gb < GL) {
+  for (int u = 0; u < WMAXB; ++u)
+    if (8 * (half + 2 * u) < GL)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t s16 = (e & 1) ? sv[u][e >> 1] >> 16 : sv[u][e >> 1] & 0xffffu;
-        const uint32_t b16 = (e & 1) ? bv[u][e >> 1] >> 16 : bv[u][e >> 1] & 0xffffu;
-        ok &= fast_ok_bits<TT>(s16, b16);
-        cstb[(8 * gb + e) * 128 + cidx] = TT::to_f32((uint16_t)b16);
-        csts[(8 * gb + e) * 128 + cidx] = (uint16_t)s16;
-      }
-    }
+      for (int q = 0; q < 4; ++q) fast_quick_add<TT>(fq, sv[u][q], bv[u][q]);
+  bool ok = fast_quick_ok<TT>(fq);
+  if (!ok) {
+    ok = true;
+#pragma unroll
+    for (int u = 0; u < WMAXB; ++u)
+      if (8 * (half + 2 * u) < GL)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          ok &= fast_ok_bits<TT>(sv[u][q] & 0xffffu, bv[u][q] & 0xffffu) &
+                fast_ok_bits<TT>(sv[u][q] >> 16, bv[u][q] >> 16);
   }
-  // This wave's stage-0 copies have landed (4 x 8 younger loads may still
-  // be in flight); the barrier makes every wave's copies visible.
-  wait_vmcnt<32>();
-  const bool fast = __syncthreads_and(ok);
-  if (fast) {
+  auto store_constants = [&](bool c0, bool scales_too) {
 #pragma unroll
     for (int u = 0; u < WMAXB; ++u) {
       const int gb = half + 2 * u;
@@ -577,12 +581,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const uint32_t s16 = (e & 1) ? sv[u][e >> 1] >> 16 : sv[u][e >> 1] & 0xffffu;
-          float* vb = cstb + (8 * gb + e) * 128 + cidx;
-          *vb = fmaf(-1024.f, TT::to_f32((uint16_t)s16), *vb);
+          const uint32_t b16 = (e & 1) ? bv[u][e >> 1] >> 16 : bv[u][e >> 1] & 0xffffu;
+          const float b = TT::to_f32((uint16_t)b16);
+          cstb[(8 * gb + e) * 128 + cidx] = c0 ? fmaf(-1024.f, TT::to_f32((uint16_t)s16), b) : b;
+          if (scales_too) csts[(8 * gb + e) * 128 + cidx] = (uint16_t)s16;
         }
       }
     }
-    __syncthreads();
+  };
+  if (ok)
+    store_constants(true, true);
+  else
+    store_constants(false, true);
+  // Vote through one LDS word per wave.  This wave's stage-0 copies have
+  // landed (4 x 8 younger loads may still be in flight); the barrier makes
+  // every wave's copies, constants and vote visible.  A bare s_barrier after
+  // explicit waits: a fenced barrier would also wait for the copies of
+  // stages 1..3.
+  __shared__ uint32_t wide_vote[4];
+  const bool wave_ok = __builtin_amdgcn_ballot_w64(!ok) == 0;
+  if (lane == 0) wide_vote[wave] = wave_ok ? 1u : 0u;
+  asm volatile("" ::: "memory");
+  wait_vm_lgkm<32>();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  const bool fast = (wide_vote[0] & wide_vote[1] & wide_vote[2] & wide_vote[3]) != 0u;
+  if (!fast) {
+    if (ok) store_constants(false, false);
+    asm volatile("" ::: "memory");
+    wait_vm_lgkm<63>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
   }
 
   // 4. Stream K.

@@ -307,6 +307,28 @@ def test_qmm_mixed_fast_and_slow_tiles(device, library, oracle, monkeypatch, dty
     assert_tol(oracle, y, ref, x, k, dtype, f"mixed wide={wide} split={split}")
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("wide,split", [(1, 2), (1, 1), (0, 1)])
+def test_qmm_zero_scales_and_biases(device, library, oracle, monkeypatch, dtype, wide, split):
+    """Zero scales or biases fail the packed exponent check but pass the
+    exact predicate, so their tiles stay on the fast dequantization; a -0
+    bias under a negative scale does not (the fast path would give +0)."""
+    monkeypatch.setenv("CPQ_QMM_WIDE", str(wide))
+    monkeypatch.setenv("CPQ_QMM_SPLIT", str(split))
+    m, n, k, gs = 130, 384, 2048, 64
+    rng = np.random.default_rng(9)
+    w_q, s, b = make_weight(rng, n, k, gs, 4, dtype)
+    s[5, 0] = 0                      # zero scale: w = b
+    b[40, 7] = 0                     # zero bias
+    s[200, 3], b[200, 3] = 0, 0      # both zero
+    s[301, 31] = s[301, 31] | 0x8000  # negative scale over a -0 bias: generic path
+    b[301, 31] = 0x8000
+    x = make_x(rng, m, k, dtype)
+    y = run_qmm(device, library, w_q, s, b, x, m, n, k, gs, 4, dtype)
+    ref = oracle.qmm_ref(x, w_q, s, b, m, n, k, gs, 4, dtype)
+    assert_tol(oracle, y, ref, x, k, dtype, f"zeros wide={wide} split={split}")
+
+
 def test_qmm_wide_split_is_deterministic(device, library, oracle, monkeypatch):
     """The split-K sum adds the parts in k order whatever order the
     workgroups finish in: repeated calls give identical bits."""
