@@ -251,28 +251,41 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
   GxCursor<BITS> ld = start;
   if (T > 0) gx_fill<BITS>(ld, ring, units, my_slabs, wstride, gstride, n, chunks, g, gs_shift);
 
-  // 2. Fast-path vote over the chunk's (column, group) pairs.
+  // 2. Fast-path vote over the chunk's (column, group) pairs: the packed
+  //    exponent check over 16-byte segments, and the exact predicate for a
+  //    thread whose segments that check does not clear.
   bool ok = true;
   if (sb_vec) {
     const int segs = G >> 3;
     for (int i0 = tid; i0 < ncols * segs; i0 += 2 * GX_THREADS) {
       u32x4 sv[2], bv[2];
+      bool live[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int i = i0 + h * GX_THREADS;
-        sv[h] = bv[h] = u32x4{0u, 0u, 0u, 0u};
-        if (i < ncols * segs) {
+        live[h] = i < ncols * segs;
+        if (live[h]) {
           const int c = i / segs, sg = i - c * segs;
           sv[h] = *reinterpret_cast<const u32x4*>(se + (size_t)(c0 + c) * G + sg * 8);
           bv[h] = *reinterpret_cast<const u32x4*>(be + (size_t)(c0 + c) * G + sg * 8);
+        } else {  // a pair the packed check accepts
+          sv[h] = bv[h] = u32x4{0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};
         }
       }
+      FastQuick fq;
+      fast_quick_init(fq);
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          ok &= fast_ok_bits<TT>(sv[h][q] & 0xffffu, bv[h][q] & 0xffffu) &
-               fast_ok_bits<TT>(sv[h][q] >> 16, bv[h][q] >> 16);
+        for (int q = 0; q < 4; ++q) fast_quick_add<TT>(fq, sv[h][q], bv[h][q]);
+      if (!fast_quick_ok<TT>(fq)) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            ok &= !live[h] | (fast_ok_bits<TT>(sv[h][q] & 0xffffu, bv[h][q] & 0xffffu) &
+                              fast_ok_bits<TT>(sv[h][q] >> 16, bv[h][q] >> 16));
+      }
     }
   } else {
     for (int i = tid; i < ncols * G; i += GX_THREADS) {

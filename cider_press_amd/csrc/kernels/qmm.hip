@@ -634,10 +634,7 @@ __global__ __launch_bounds__(256 * MH) __attribute__((amdgpu_waves_per_eu(MH, MH
   //    its column per block, all blocks' loads in flight together.
   uint32_t* cst = reinterpret_cast<uint32_t*>(smem + cst_base);
   bool ok = true;
-  auto put = [&](int c, int gi, uint32_t sv, uint32_t bv) {
-    ok &= fast_ok_bits<TT>(sv, bv);
-    cst[(gi * 16 + (c & 15)) * 4 + (c >> 4)] = sv | (bv << 16);
-  };
+  auto put = [&](int c, int gi, uint32_t sv, uint32_t bv) { cst[(gi * 16 + (c & 15)) * 4 + (c >> 4)] = sv | (bv << 16); };
   if (sb_vec) {
     constexpr int MAXB = QMAX_GROUPS / 8 / (NT / 64);  // 8-group blocks per thread
     const int c = tid & 63, col = min(col0 + c, n - 1);
@@ -651,20 +648,39 @@ __global__ __launch_bounds__(256 * MH) __attribute__((amdgpu_waves_per_eu(MH, MH
         bv[u] = *reinterpret_cast<const u32x4*>(biases + (size_t)col * G + gb * 8);
       }
     }
+    // Packed exponent check over the thread's blocks; the exact predicate
+    // per group only when that one does not clear them.
+    FastQuick fq;
+    fast_quick_init(fq);
 #pragma unroll
     for (int u = 0; u < MAXB; ++u) {
       const int gb = (tid >> 6) + (NT / 64) * u;
       if (gb < nblk) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) fast_quick_add<TT>(fq, sv[u][q], bv[u][q]);
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           put(c, gb * 8 + e, (e & 1) ? sv[u][e >> 1] >> 16 : sv[u][e >> 1] & 0xffffu,
               (e & 1) ? bv[u][e >> 1] >> 16 : bv[u][e >> 1] & 0xffffu);
       }
     }
+    if (!fast_quick_ok<TT>(fq)) {
+#pragma unroll
+      for (int u = 0; u < MAXB; ++u) {
+        const int gb = (tid >> 6) + (NT / 64) * u;
+        if (gb < nblk) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            ok &= fast_ok_bits<TT>(sv[u][q] & 0xffffu, bv[u][q] & 0xffffu) &
+                  fast_ok_bits<TT>(sv[u][q] >> 16, bv[u][q] >> 16);
+        }
+      }
+    }
   } else {
     for (int it = tid; it < 64 * G; it += NT) {
       const int c = it & 63, gi = it >> 6;
       const size_t off = (size_t)min(col0 + c, n - 1) * G + gi;
+      ok &= fast_ok_bits<TT>(scales[off], biases[off]);
       put(c, gi, scales[off], biases[off]);
     }
   }

@@ -81,9 +81,25 @@ __device__ __forceinline__ bool slab_consts_store(const uint16_t* __restrict__ s
                                                   int GP) {
   bool ok = true;
   auto put = [&](int c, int gi, uint32_t sv, uint32_t bv) {
-    ok &= fast_ok_bits<TT>(sv, bv);
     const float sf = TT::to_f32((uint16_t)sv), bf = TT::to_f32((uint16_t)bv);
     gc[c * GP + gi] = f32x4{sf, bf, fmaf(-1024.f, sf, bf), fmaf(-64.f, sf, bf)};
+  };
+  // A 16-byte segment (8 groups): the packed exponent check, and the exact
+  // predicate per group only when that one does not clear the segment.
+  auto put8 = [&](int c, int sg, const u32x4& s4, const u32x4& b4) {
+    FastQuick fq;
+    fast_quick_init(fq);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) fast_quick_add<TT>(fq, s4[q], b4[q]);
+    if (!fast_quick_ok<TT>(fq)) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        ok &= fast_ok_bits<TT>(s4[q] & 0xffffu, b4[q] & 0xffffu) & fast_ok_bits<TT>(s4[q] >> 16, b4[q] >> 16);
+    }
+#pragma unroll
+    for (int h = 0; h < 8; ++h)
+      put(c, sg * 8 + h, (h & 1) ? s4[h >> 1] >> 16 : s4[h >> 1] & 0xffffu,
+          (h & 1) ? b4[h >> 1] >> 16 : b4[h >> 1] & 0xffffu);
   };
   if (vec) {
     const int segs = G >> 3;
@@ -92,10 +108,7 @@ __device__ __forceinline__ bool slab_consts_store(const uint16_t* __restrict__ s
       const int i = threadIdx.x + NT * t;
       if (i < 16 * segs) {
         const int c = i / segs, sg = i - c * segs;
-#pragma unroll
-        for (int h = 0; h < 8; ++h)
-          put(c, sg * 8 + h, (h & 1) ? sc.sv[t][h >> 1] >> 16 : sc.sv[t][h >> 1] & 0xffffu,
-              (h & 1) ? sc.bv[t][h >> 1] >> 16 : sc.bv[t][h >> 1] & 0xffffu);
+        put8(c, sg, sc.sv[t], sc.bv[t]);
       }
     }
     for (int i = threadIdx.x + NT * kConstSlots; i < 16 * segs; i += NT) {
@@ -105,10 +118,7 @@ __device__ __forceinline__ bool slab_consts_store(const uint16_t* __restrict__ s
         s4 = *reinterpret_cast<const u32x4*>(scales + (size_t)(n0 + c) * G + sg * 8);
         b4 = *reinterpret_cast<const u32x4*>(biases + (size_t)(n0 + c) * G + sg * 8);
       }
-#pragma unroll
-      for (int h = 0; h < 8; ++h)
-        put(c, sg * 8 + h, (h & 1) ? s4[h >> 1] >> 16 : s4[h >> 1] & 0xffffu,
-            (h & 1) ? b4[h >> 1] >> 16 : b4[h >> 1] & 0xffffu);
+      put8(c, sg, s4, b4);
     }
   } else {
     for (int it = threadIdx.x; it < 16 * G; it += NT) {
@@ -118,6 +128,7 @@ __device__ __forceinline__ bool slab_consts_store(const uint16_t* __restrict__ s
         sv = scales[(size_t)(n0 + c) * G + gi];
         bv = biases[(size_t)(n0 + c) * G + gi];
       }
+      ok &= fast_ok_bits<TT>(sv, bv);
       put(c, gi, sv, bv);
     }
   }
