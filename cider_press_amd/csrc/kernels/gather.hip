@@ -75,23 +75,85 @@ struct GxCursor {
   }
 };
 
-template <int BITS>
+// Scale / bias words of QS consecutive steps (a "quad"), loaded at its first
+// step when QS > 1: the QS * 128 / GSQ groups of the lane's column that the
+// quad's 4 QS chunks span, in one 8- or 16-byte load each (QS = 1: one 2-byte
+// load of each per step, in the step itself).  The quad's first unit is a
+// multiple of QS, so the vector is aligned and inside the column's row.
+struct GxSb {
+  u32x4 s, b;
+};
+
+template <int QS, int GSQ>
+struct GxQuad {
+  static constexpr int kBytes = QS > 1 ? QS * 128 / GSQ * 2 : 0;
+  static_assert(QS == 1 || kBytes == 8 || kBytes == 16, "quad vector of 8 or 16 bytes");
+};
+
+template <int BITS, int QS>
 __device__ __forceinline__ void gx_load(const GxCursor<BITS>& c, GxStep<BITS>& dst, int chunks, int g,
                                         int gs_shift) {
   const int ch = min(4 * c.u + g, chunks - 1);
   load_chunk<BITS>(c.wrow, (size_t)ch, dst.w);
-  const int gi = (ch << 5) >> gs_shift;
-  dst.s = c.srow[gi];
-  dst.b = c.brow[gi];
+  if constexpr (QS == 1) {
+    const int gi = (ch << 5) >> gs_shift;
+    dst.s = c.srow[gi];
+    dst.b = c.brow[gi];
+  }
+}
+
+template <int BITS, int QS, int GSQ>
+__device__ __forceinline__ void gx_load_sb(const GxCursor<BITS>& c, GxSb& v) {
+  const int gi = (c.u * 128) / GSQ;  // first group of the quad
+  if constexpr (GxQuad<QS, GSQ>::kBytes == 16) {
+    v.s = *reinterpret_cast<const u32x4*>(c.srow + gi);
+    v.b = *reinterpret_cast<const u32x4*>(c.brow + gi);
+  } else {
+    const u32x2 s2 = *reinterpret_cast<const u32x2*>(c.srow + gi);
+    const u32x2 b2 = *reinterpret_cast<const u32x2*>(c.brow + gi);
+    v.s = u32x4{s2[0], s2[1], 0u, 0u};
+    v.b = u32x4{b2[0], b2[1], 0u, 0u};
+  }
+}
+
+// The 16-bit scale or bias of quad step I for this lane (lane group g): group
+// (128 I + 32 g) / GSQ of the quad.  GSQ = 64: word I, half g / 2 (per lane,
+// `sel` picks it); GSQ = 128: word I / 2, half I % 2.
+// (I is a constant once the step loop is unrolled.)
+template <typename TT, int GSQ>
+__device__ __forceinline__ float gx_sb_f32(const u32x4& v, int I, uint32_t sel) {
+  if constexpr (GSQ == 64) {
+    const uint32_t word = v[I];
+    if constexpr (Sig16<TT>::bf16)
+      return __uint_as_float(__builtin_amdgcn_perm(word, word, sel));
+    else
+      return TT::to_f32((uint16_t)__builtin_amdgcn_perm(word, word, sel));
+  } else {
+    const uint32_t word = v[I >> 1];
+    return TT::to_f32((uint16_t)((I & 1) ? word >> 16 : word & 0xffffu));
+  }
+}
+
+// Byte selector of gx_sb_f32 for lane group g (GSQ = 64): the 16-bit half
+// g / 2 into the high half (bf16: the f32 bits) or the low half (f16).
+template <typename TT>
+__device__ __forceinline__ uint32_t gx_sb_sel(int g) {
+  if constexpr (Sig16<TT>::bf16)
+    return (g >> 1) ? 0x03020c0cu : 0x01000c0cu;
+  else
+    return (g >> 1) ? 0x0c0c0302u : 0x0c0c0100u;
 }
 
 // The first GX_PF steps of a wave's weight stream; `ld` ends past them.
-template <int BITS>
-__device__ __forceinline__ void gx_fill(GxCursor<BITS>& ld, GxStep<BITS> (&ring)[GX_PF], int units, int my_slabs,
-                                        size_t wstride, size_t gstride, int n, int chunks, int g, int gs_shift) {
+template <int BITS, int QS, int GSQ>
+__device__ __forceinline__ void gx_fill(GxCursor<BITS>& ld, GxStep<BITS> (&ring)[GX_PF],
+                                        GxSb (&sbq)[GX_PF / QS], int units, int my_slabs, size_t wstride,
+                                        size_t gstride, int n, int chunks, int g, int gs_shift) {
 #pragma unroll
   for (int p = 0; p < GX_PF; ++p) {
-    gx_load<BITS>(ld, ring[p], chunks, g, gs_shift);
+    gx_load<BITS, QS>(ld, ring[p], chunks, g, gs_shift);
+    if constexpr (QS > 1)
+      if (p % QS == 0) gx_load_sb<BITS, QS, GSQ>(ld, sbq[p / QS]);
     ld.next(units, my_slabs, wstride, gstride, n);
   }
 }
@@ -114,26 +176,41 @@ __device__ __forceinline__ int wave_lower_bound(const uint32_t* __restrict__ a, 
   return lo;
 }
 
-template <typename TT, int BITS, int MB, bool FAST>
-__device__ __forceinline__ void gx_stream(GxCursor<BITS> ld, GxCursor<BITS> cp, GxStep<BITS> (&ring)[GX_PF], int T,
-                                          int units, int my_slabs, size_t wstride, size_t gstride, int n, int chunks,
-                                          int gs_shift, int g, int nl, const unsigned char* xs, int k,
-                                          const GxShared& sh, int mbl, uint16_t* __restrict__ y) {
+template <typename TT, int BITS, int MB, bool FAST, int QS, int GSQ>
+__device__ __forceinline__ void gx_stream(GxCursor<BITS> ld, GxCursor<BITS> cp, GxStep<BITS> (&ring)[GX_PF],
+                                          GxSb (&sbq)[GX_PF / QS], int T, int units, int my_slabs, size_t wstride,
+                                          size_t gstride, int n, int chunks, int gs_shift, int g, int nl,
+                                          const unsigned char* xs, int k, const GxShared& sh, int mbl,
+                                          uint16_t* __restrict__ y) {
   const int TP = (T + GX_PF - 1) / GX_PF * GX_PF;
+  const uint32_t sel = gx_sb_sel<TT>(g);
   f32x4 acc[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  GxSb curq;
   for (int t0 = 0; t0 < TP; t0 += GX_PF) {
 #pragma unroll
     for (int p = 0; p < GX_PF; ++p) {
       const int t = t0 + p;
       const GxStep<BITS> cur = ring[p];
-      gx_load<BITS>(ld, ring[p], chunks, g, gs_shift);  // clamped past the end: no branch, no wait
+      if constexpr (QS > 1)
+        if (p % QS == 0) curq = sbq[p / QS];
+      gx_load<BITS, QS>(ld, ring[p], chunks, g, gs_shift);  // clamped past the end: no branch, no wait
+      if constexpr (QS > 1)
+        if (p % QS == 0) gx_load_sb<BITS, QS, GSQ>(ld, sbq[p / QS]);
       ld.next(units, my_slabs, wstride, gstride, n);
       const int c = 4 * cp.u + g;
       const bool live = t < T && c < chunks && cp.col < n;
-      const float sf = live ? TT::to_f32((uint16_t)cur.s) : 0.f;
-      const float bf = live ? TT::to_f32((uint16_t)cur.b) : 0.f;
+      float sf = 0.f, bf = 0.f;
+      if constexpr (QS == 1) {
+        sf = TT::to_f32((uint16_t)cur.s);
+        bf = TT::to_f32((uint16_t)cur.b);
+      } else {
+        sf = gx_sb_f32<TT, GSQ>(curq.s, p % QS, sel);
+        bf = gx_sb_f32<TT, GSQ>(curq.b, p % QS, sel);
+      }
+      sf = live ? sf : 0.f;
+      bf = live ? bf : 0.f;
       const float s16 = sf * 0.0625f;
       const float c0 = FAST ? fmaf(-1024.f, sf, bf) : 0.f, c1 = FAST ? fmaf(-64.f, sf, bf) : 0.f;
       u32x4 bop[4];
@@ -173,7 +250,7 @@ __device__ __forceinline__ void gx_stream(GxCursor<BITS> ld, GxCursor<BITS> cp, 
   }
 }
 
-template <typename TT, int BITS, int MB>
+template <typename TT, int BITS, int MB, int QS, int GSQ>
 __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, int x_rows,
@@ -248,8 +325,9 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
   start.srow = se + (size_t)col0 * G;
   start.brow = be + (size_t)col0 * G;
   GxStep<BITS> ring[GX_PF];
+  GxSb sbq[GX_PF / QS];
   GxCursor<BITS> ld = start;
-  if (T > 0) gx_fill<BITS>(ld, ring, units, my_slabs, wstride, gstride, n, chunks, g, gs_shift);
+  if (T > 0) gx_fill<BITS, QS, GSQ>(ld, ring, sbq, units, my_slabs, wstride, gstride, n, chunks, g, gs_shift);
 
   // 2. Fast-path vote over the chunk's (column, group) pairs: the packed
   //    exponent check over 16-byte segments, and the exact predicate for a
@@ -359,25 +437,25 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
     if (T > 0) {
       if (p0 > 0) {  // a further pass streams the weights again
         ld = start;
-        gx_fill<BITS>(ld, ring, units, my_slabs, wstride, gstride, n, chunks, g, gs_shift);
+        gx_fill<BITS, QS, GSQ>(ld, ring, sbq, units, my_slabs, wstride, gstride, n, chunks, g, gs_shift);
       }
       if (fast)
-        gx_stream<TT, BITS, MB, true>(ld, start, ring, T, units, my_slabs, wstride, gstride, n, chunks, gs_shift,
+        gx_stream<TT, BITS, MB, true, QS, GSQ>(ld, start, ring, sbq, T, units, my_slabs, wstride, gstride, n, chunks, gs_shift,
                                       g, nl, xs, k, sh, mbl, y);
       else
-        gx_stream<TT, BITS, MB, false>(ld, start, ring, T, units, my_slabs, wstride, gstride, n, chunks,
+        gx_stream<TT, BITS, MB, false, QS, GSQ>(ld, start, ring, sbq, T, units, my_slabs, wstride, gstride, n, chunks,
                                        gs_shift, g, nl, xs, k, sh, mbl, y);
     }
     __syncthreads();  // LDS rows / activations are rewritten by the next pass
   }
 }
 
-template <typename TT, int BITS, int MB>
-hipError_t launch_mb(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
-                     const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
-                     int gs_shift, int n_chunks, int nc) {
+template <typename TT, int BITS, int MB, int QS, int GSQ>
+hipError_t launch_q(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
+                    const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
+                    int gs_shift, int n_chunks, int nc, int sb_vec) {
   static const hipError_t attr = [] {
-    const void* fn = reinterpret_cast<const void*>(&gather_expert_kernel<TT, BITS, MB>);
+    const void* fn = reinterpret_cast<const void*>(&gather_expert_kernel<TT, BITS, MB, QS, GSQ>);
     hipFuncAttributes fa;
     hipError_t e = hipFuncGetAttributes(&fa, fn);
     if (e != hipSuccess) return e;
@@ -386,14 +464,35 @@ hipError_t launch_mb(hipStream_t s, const QuantArgs& q, const void* x, int x_row
   }();
   if (attr != hipSuccess) return attr;
   const size_t lds = (size_t)16 * MB * k * 2;
-  const int G = k / q.gs;
-  const int sb_vec = (G % 8 == 0) && (reinterpret_cast<uintptr_t>(q.scales) % 16 == 0) &&
-                     (reinterpret_cast<uintptr_t>(q.biases) % 16 == 0);
-  hipLaunchKernelGGL((gather_expert_kernel<TT, BITS, MB>), dim3((unsigned)n_chunks, (unsigned)n_experts),
+  hipLaunchKernelGGL((gather_expert_kernel<TT, BITS, MB, QS, GSQ>), dim3((unsigned)n_chunks, (unsigned)n_experts),
                      dim3(GX_THREADS), lds, s, q.w, static_cast<const uint16_t*>(q.scales),
                      static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x), x_rows, lhs,
                      rhs, n_rows, static_cast<uint16_t*>(y), n, k, gs_shift, (int)sorted, nc, sb_vec);
   return hipGetLastError();
+}
+
+// Scale / bias quads: 4 steps per 16-byte load (gs 64) or 8-byte load (gs
+// 128) when a slab's units divide by 4, else 2 steps per 8-byte load (gs 64),
+// else per-step 2-byte loads.  Alignment: row starts are multiples of the
+// vector (G a multiple of its groups) and the base pointers aligned to it.
+template <typename TT, int BITS, int MB>
+hipError_t launch_mb(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
+                     const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
+                     int gs_shift, int n_chunks, int nc) {
+  const int G = k / q.gs, units = k / 128;
+  const uintptr_t al = reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases);
+  const int sb_vec = (G % 8 == 0) && (al % 16 == 0);
+  static const int forced = env_int("CPQ_GATHER_QS", 0);
+#define CPQ_GXQ(QS, GSQ)                                                                                  \
+  return launch_q<TT, BITS, MB, QS, GSQ>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted,   \
+                                         gs_shift, n_chunks, nc, sb_vec)
+  if (forced != 1) {
+    if (q.gs == 64 && units % 4 == 0 && al % 16 == 0 && forced != 2) CPQ_GXQ(4, 64);
+    if (q.gs == 64 && units % 2 == 0 && al % 8 == 0) CPQ_GXQ(2, 64);
+    if (q.gs == 128 && units % 4 == 0 && al % 8 == 0) CPQ_GXQ(4, 128);
+  }
+  CPQ_GXQ(1, 64);
+#undef CPQ_GXQ
 }
 
 template <typename TT, int BITS>

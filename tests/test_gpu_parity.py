@@ -442,6 +442,30 @@ def test_gather_expert_kernel_passes(device, library, oracle, bits, k, dtype):
     assert_tol(oracle, y, ref, x, k, dtype, f"gather expert {bits}b K={k}")
 
 
+@pytest.mark.parametrize("gs,k,dtype,bits", [
+    (64, 768, "bf16", 4),     # 6 units per slab: scale / bias pairs of steps (8-byte loads)
+    (64, 768, "f16", 4),
+    (64, 1536, "bf16", 8),    # 12 units: quads of 4 steps (16-byte loads)
+    (128, 1024, "bf16", 4),   # quads of 4 steps, gs 128 (8-byte loads)
+    (128, 1024, "f16", 4),
+    (128, 768, "bf16", 4),    # 6 units at gs 128: per-step loads
+    (64, 384, "bf16", 4),     # 3 units: per-step loads
+    (32, 1024, "bf16", 4),    # gs 32: per-step loads
+])
+def test_gather_scale_bias_step_groupings(device, library, oracle, gs, k, dtype, bits):
+    """Every scale / bias load grouping of the expert-major kernel, with
+    several slabs per wave (512 columns, 3 experts) and sorted routing."""
+    rng = np.random.default_rng(gs + k + bits)
+    e, n, rows = 3, 512, 60
+    w_q, s, b = _experts(rng, e, n, k, gs, bits, dtype)
+    x = make_x(rng, 30, k, dtype)
+    rhs = np.sort(rng.integers(0, e, size=rows)).astype(np.uint32)
+    lhs = rng.integers(0, 30, size=rows).astype(np.uint32)
+    y = run_gather(device, library, x, w_q, s, b, lhs, rhs, rows, n, k, e, gs, bits, dtype, True)
+    ref = oracle.gather_qmm_ref(x, lhs, rhs, w_q, s, b, rows, n, k, gs, bits, dtype)
+    assert_tol(oracle, y, ref, x, k, dtype, f"gather gs={gs} K={k} {dtype} {bits}b")
+
+
 def test_gather_out_of_range_index_reported(device, library, oracle):
     rng = np.random.default_rng(23)
     e, n, k, gs, rows = 4, 32, 128, 64, 8
