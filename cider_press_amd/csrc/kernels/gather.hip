@@ -329,48 +329,46 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
   GxCursor<BITS> ld = start;
   if (T > 0) gx_fill<BITS, QS, GSQ>(ld, ring, sbq, units, my_slabs, wstride, gstride, n, chunks, g, gs_shift);
 
-  // 2. Fast-path vote over the chunk's (column, group) pairs: the packed
-  //    exponent check over 16-byte segments, and the exact predicate for a
-  //    thread whose segments that check does not clear.
+  // 2. Fast-path vote over the chunk's (column, group) pairs.  The chunk's
+  //    columns are consecutive rows of the expert's [n, G] tables, so its
+  //    pairs are one contiguous run of ncols * G entries: 16-byte segments
+  //    (when the run starts 16-byte aligned) get the packed exponent check,
+  //    and the exact predicate where that one does not clear a thread's
+  //    segments; the tail and unaligned runs go pair by pair.
   bool ok = true;
-  if (sb_vec) {
-    const int segs = G >> 3;
-    for (int i0 = tid; i0 < ncols * segs; i0 += 2 * GX_THREADS) {
-      u32x4 sv[2], bv[2];
-      bool live[2];
+  const size_t run0 = (size_t)c0 * G;
+  const int run = ncols * G;
+  const int nvec = sb_vec ? run >> 3 : 0;
+  for (int i0 = tid; i0 < nvec; i0 += 2 * GX_THREADS) {
+    u32x4 sv[2], bv[2];
+    bool live[2];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int i = i0 + h * GX_THREADS;
-        live[h] = i < ncols * segs;
-        if (live[h]) {
-          const int c = i / segs, sg = i - c * segs;
-          sv[h] = *reinterpret_cast<const u32x4*>(se + (size_t)(c0 + c) * G + sg * 8);
-          bv[h] = *reinterpret_cast<const u32x4*>(be + (size_t)(c0 + c) * G + sg * 8);
-        } else {  // a pair the packed check accepts
-          sv[h] = bv[h] = u32x4{0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};
-        }
+    for (int h = 0; h < 2; ++h) {
+      const int i = i0 + h * GX_THREADS;
+      live[h] = i < nvec;
+      if (live[h]) {
+        sv[h] = *reinterpret_cast<const u32x4*>(se + run0 + (size_t)i * 8);
+        bv[h] = *reinterpret_cast<const u32x4*>(be + run0 + (size_t)i * 8);
+      } else {  // a pair the packed check accepts
+        sv[h] = bv[h] = u32x4{0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};
       }
-      FastQuick fq;
-      fast_quick_init(fq);
+    }
+    FastQuick fq;
+    fast_quick_init(fq);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) fast_quick_add<TT>(fq, sv[h][q], bv[h][q]);
+    if (!fast_quick_ok<TT>(fq)) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) fast_quick_add<TT>(fq, sv[h][q], bv[h][q]);
-      if (!fast_quick_ok<TT>(fq)) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            ok &= !live[h] | (fast_ok_bits<TT>(sv[h][q] & 0xffffu, bv[h][q] & 0xffffu) &
-                              fast_ok_bits<TT>(sv[h][q] >> 16, bv[h][q] >> 16));
-      }
-    }
-  } else {
-    for (int i = tid; i < ncols * G; i += GX_THREADS) {
-      const int c = i / G, gi = i - c * G;
-      ok &= fast_ok_bits<TT>(se[(size_t)(c0 + c) * G + gi], be[(size_t)(c0 + c) * G + gi]);
+        for (int q = 0; q < 4; ++q)
+          ok &= !live[h] | (fast_ok_bits<TT>(sv[h][q] & 0xffffu, bv[h][q] & 0xffffu) &
+                            fast_ok_bits<TT>(sv[h][q] >> 16, bv[h][q] >> 16));
     }
   }
+  for (int i = 8 * nvec + tid; i < run; i += GX_THREADS) ok &= fast_ok_bits<TT>(se[run0 + i], be[run0 + i]);
   bool fast = __syncthreads_and(ok);
   if constexpr (BITS != 4 && BITS != 8) fast = false;
 
@@ -481,7 +479,8 @@ hipError_t launch_mb(hipStream_t s, const QuantArgs& q, const void* x, int x_row
                      int gs_shift, int n_chunks, int nc) {
   const int G = k / q.gs, units = k / 128;
   const uintptr_t al = reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases);
-  const int sb_vec = (G % 8 == 0) && (al % 16 == 0);
+  // Vote runs start at (e n + c0) G entries, c0 a multiple of 128.
+  const int sb_vec = ((long)n * G % 8 == 0) && (al % 16 == 0);
   static const int forced = env_int("CPQ_GATHER_QS", 0);
 #define CPQ_GXQ(QS, GSQ)                                                                                  \
   return launch_q<TT, BITS, MB, QS, GSQ>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted,   \

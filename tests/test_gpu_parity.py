@@ -442,21 +442,22 @@ def test_gather_expert_kernel_passes(device, library, oracle, bits, k, dtype):
     assert_tol(oracle, y, ref, x, k, dtype, f"gather expert {bits}b K={k}")
 
 
-@pytest.mark.parametrize("gs,k,dtype,bits", [
-    (64, 768, "bf16", 4),     # 6 units per slab: scale / bias pairs of steps (8-byte loads)
-    (64, 768, "f16", 4),
-    (64, 1536, "bf16", 8),    # 12 units: quads of 4 steps (16-byte loads)
-    (128, 1024, "bf16", 4),   # quads of 4 steps, gs 128 (8-byte loads)
-    (128, 1024, "f16", 4),
-    (128, 768, "bf16", 4),    # 6 units at gs 128: per-step loads
-    (64, 384, "bf16", 4),     # 3 units: per-step loads
-    (32, 1024, "bf16", 4),    # gs 32: per-step loads
+@pytest.mark.parametrize("gs,k,dtype,bits,n", [
+    (64, 768, "bf16", 4, 512),     # 6 units per slab: scale / bias pairs of steps (8-byte loads)
+    (64, 768, "f16", 4, 512),
+    (64, 1536, "bf16", 8, 512),    # 12 units: quads of 4 steps (16-byte loads)
+    (128, 1024, "bf16", 4, 512),   # quads of 4 steps, gs 128 (8-byte loads)
+    (128, 1024, "f16", 4, 512),
+    (128, 768, "bf16", 4, 512),    # 6 units at gs 128: per-step loads
+    (64, 384, "bf16", 4, 512),     # 3 units: per-step loads
+    (32, 1024, "bf16", 4, 512),    # gs 32: per-step loads
+    (128, 384, "bf16", 4, 100),    # n G = 300: the vote reads pair by pair; ragged last slab
 ])
-def test_gather_scale_bias_step_groupings(device, library, oracle, gs, k, dtype, bits):
+def test_gather_scale_bias_step_groupings(device, library, oracle, gs, k, dtype, bits, n):
     """Every scale / bias load grouping of the expert-major kernel, with
-    several slabs per wave (512 columns, 3 experts) and sorted routing."""
-    rng = np.random.default_rng(gs + k + bits)
-    e, n, rows = 3, 512, 60
+    several slabs per wave (3 experts) and sorted routing."""
+    rng = np.random.default_rng(gs + k + bits + n)
+    e, rows = 3, 60
     w_q, s, b = _experts(rng, e, n, k, gs, bits, dtype)
     x = make_x(rng, 30, k, dtype)
     rhs = np.sort(rng.integers(0, e, size=rows)).astype(np.uint32)
