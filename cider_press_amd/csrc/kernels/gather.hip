@@ -339,11 +339,11 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
   const size_t run0 = (size_t)c0 * G;
   const int run = ncols * G;
   const int nvec = sb_vec ? run >> 3 : 0;
-  for (int i0 = tid; i0 < nvec; i0 += 2 * GX_THREADS) {
-    u32x4 sv[2], bv[2];
-    bool live[2];
+  for (int i0 = tid; i0 < nvec; i0 += 4 * GX_THREADS) {
+    u32x4 sv[4], bv[4];
+    bool live[4];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < 4; ++h) {
       const int i = i0 + h * GX_THREADS;
       live[h] = i < nvec;
       if (live[h]) {
@@ -356,12 +356,12 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
     FastQuick fq;
     fast_quick_init(fq);
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < 4; ++h)
 #pragma unroll
       for (int q = 0; q < 4; ++q) fast_quick_add<TT>(fq, sv[h][q], bv[h][q]);
     if (!fast_quick_ok<TT>(fq)) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < 4; ++h)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
           ok &= !live[h] | (fast_ok_bits<TT>(sv[h][q] & 0xffffu, bv[h][q] & 0xffffu) &
@@ -403,24 +403,28 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
     __syncthreads();
 
     // 4. Activation rows into LDS in the dequantizer's slot order, 16-byte
-    //    chunk q of row i at i*K*2 + (q ^ (i & 15))*16.
+    //    chunk q of row i at i*K*2 + (q ^ (i & 15))*16.  Only the pass's
+    //    rows are staged, 8 loads per thread in flight: the other rows of
+    //    its 16-row blocks keep stale LDS bytes, which reach only their own
+    //    output rows (MFMA rows are independent), and those are not stored.
     const int kq = k >> 3;  // 16-byte chunks per row
-    for (int idx = tid; idx < R * kq; idx += GX_THREADS * 4) {
-      u32x4 v[4];
+    const int nst = min(R, total - p0) * kq;
+    for (int idx = tid; idx < nst; idx += GX_THREADS * 8) {
+      u32x4 v[8];
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
+      for (int h = 0; h < 8; ++h) {
         const int id = idx + h * GX_THREADS;
         v[h] = u32x4{0u, 0u, 0u, 0u};
-        if (id < R * kq) {
+        if (id < nst) {
           const int i = id / kq, q = id - i * kq;
           const int xi = sh.xrow[i];
           if (xi >= 0) v[h] = *reinterpret_cast<const u32x4*>(x + (size_t)xi * k + (size_t)q * 8);
         }
       }
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
+      for (int h = 0; h < 8; ++h) {
         const int id = idx + h * GX_THREADS;
-        if (id < R * kq) {
+        if (id < nst) {
           const int i = id / kq, q = id - i * kq;
           *reinterpret_cast<u32x4*>(xs + (size_t)i * k * 2 + (size_t)((q ^ (i & 15)) * 16)) =
               interleave_x<BITS>(v[h]);
