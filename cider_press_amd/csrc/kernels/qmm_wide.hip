@@ -177,8 +177,11 @@ __device__ __forceinline__ u32x4 wide_dequant(uint32_t word, float sf, float cb)
   }
 }
 
-// The fast dequantization cut into 6 chunks of at most 4 VALU instructions,
-// issued between MFMAs so the VALU work fills the matrix pipe's issue gaps.
+// The fast dequantization cut into 4 chunks, one per MFMA slot of a block, so
+// the VALU work fills the matrix pipe's issue gaps.  The nibble extractions
+// all go first: v_fma_mix reads its 16-bit source 2 wait states after the
+// VALU write at the earliest, and with the MFMA slot in between no chunk
+// needs a wait-state nop.
 struct WideDeq {
   uint32_t word, w8, p0, p1, p2, p3, o0, o1, o2, o3;
   float sf, cb, c1, f0, f1, f2, f3, f4, f5, f6, f7;
@@ -190,25 +193,23 @@ __device__ __forceinline__ void wide_deq_step(WideDeq& d) {
     d.c1 = fmaf(960.f, d.sf, d.cb);
     d.w8 = d.word >> 8;
     d.p0 = and_or(d.word, 0x000F000Fu, 0x64006400u);
-  } else if constexpr (K == 1) {
     d.p1 = and_or(d.word, 0x00F000F0u, 0x54005400u);
-    d.f0 = fmaf(d.sf, f16lo(d.p0), d.cb);
-    d.f1 = fmaf(d.sf, f16lo(d.p1), d.c1);
-  } else if constexpr (K == 2) {
-    d.o0 = TT::pack2(d.f0, d.f1);
-    d.f4 = fmaf(d.sf, f16hi(d.p0), d.cb);
-    d.f5 = fmaf(d.sf, f16hi(d.p1), d.c1);
-  } else if constexpr (K == 3) {
-    d.o2 = TT::pack2(d.f4, d.f5);
     d.p2 = and_or(d.w8, 0x000F000Fu, 0x64006400u);
     d.p3 = and_or(d.w8, 0x00F000F0u, 0x54005400u);
-  } else if constexpr (K == 4) {
+  } else if constexpr (K == 1) {
+    d.f0 = fmaf(d.sf, f16lo(d.p0), d.cb);
+    d.f1 = fmaf(d.sf, f16lo(d.p1), d.c1);
+    d.f4 = fmaf(d.sf, f16hi(d.p0), d.cb);
+    d.f5 = fmaf(d.sf, f16hi(d.p1), d.c1);
+  } else if constexpr (K == 2) {
+    d.o0 = TT::pack2(d.f0, d.f1);
+    d.o2 = TT::pack2(d.f4, d.f5);
     d.f2 = fmaf(d.sf, f16lo(d.p2), d.cb);
     d.f3 = fmaf(d.sf, f16lo(d.p3), d.c1);
-    d.f6 = fmaf(d.sf, f16hi(d.p2), d.cb);
-  } else if constexpr (K == 5) {
-    d.f7 = fmaf(d.sf, f16hi(d.p3), d.c1);
+  } else if constexpr (K == 3) {
     d.o1 = TT::pack2(d.f2, d.f3);
+    d.f6 = fmaf(d.sf, f16hi(d.p2), d.cb);
+    d.f7 = fmaf(d.sf, f16hi(d.p3), d.c1);
     d.o3 = TT::pack2(d.f6, d.f7);
   }
 }
@@ -318,19 +319,13 @@ __device__ __forceinline__ void wide_fast_blocks(const WideGeom& g, int s, u32x4
     for (int i = 0; i < 4; ++i) {
       wide_mfma<TT>(acc[i][JB], a[i][TS], bop[O]);
       if constexpr (HAS) {
-        if (i == 0) {
-          wide_deq_step<TT, 0>(d);
-          wide_deq_step<TT, 1>(d);
-        }
-        if (i == 1) {
-          wide_deq_step<TT, 2>(d);
+        if (i == 0) wide_deq_step<TT, 0>(d);
+        if (i == 1) wide_deq_step<TT, 1>(d);
+        if (i == 2) wide_deq_step<TT, 2>(d);
+        if (i == 3) {
           wide_deq_step<TT, 3>(d);
+          bop[TGT] = u32x4{d.o0, d.o1, d.o2, d.o3};
         }
-        if (i == 2) {
-          wide_deq_step<TT, 4>(d);
-          wide_deq_step<TT, 5>(d);
-        }
-        if (i == 3) bop[TGT] = u32x4{d.o0, d.o1, d.o2, d.o3};
       }
       if constexpr (O >= 6 && NEXT) a[i][O - 6] = *reinterpret_cast<const u32x4*>(slot + g.a_off[O - 6] + i * 8192);
       if (i == 3) {
