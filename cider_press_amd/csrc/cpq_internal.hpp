@@ -125,12 +125,14 @@ hipError_t zero_words(hipStream_t s, void* p, size_t n_words);
 hipError_t session_scratch(cpq_commands* cmds, size_t bytes, void** out);
 
 // Routed experts, expert-major kernel (4/8-bit, K % 128 == 0): one
-// workgroup per (expert, column chunk).  gather_expert_supported says whether
+// workgroup per (expert, column chunk); it also validates the indices (bad
+// rows zeroed, bad rows and sorted-order descents counted into *status).  gather_expert_supported says whether
 // it applies; launch_gather_qmm uses it when it does.
 bool gather_expert_supported(int bits, int n_rows, int k);
 hipError_t launch_gather_expert(hipStream_t s, const QuantArgs& q, const void* x, int x_rows,
                                 const uint32_t* lhs, const uint32_t* rhs, int n_rows, void* y,
-                                int n_experts, int n, int k, bool sorted, int cu_count);
+                                int n_experts, int n, int k, bool sorted, int cu_count,
+                                unsigned int* status);
 
 // Routed experts.
 hipError_t launch_gather_qmm(hipStream_t s, const QuantArgs& q, const void* x, int x_rows,

@@ -255,7 +255,8 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, int x_rows,
     const uint32_t* __restrict__ lhs, const uint32_t* __restrict__ rhs, int n_rows,
-    uint16_t* __restrict__ y, int n, int k, int gs_shift, int sorted, int nc, int sb_vec) {
+    uint16_t* __restrict__ y, int n, int k, int gs_shift, int sorted, int nc, int sb_vec,
+    unsigned int* __restrict__ status) {
   constexpr int R = 16 * MB;
   __shared__ GxShared sh;
   extern __shared__ __attribute__((aligned(16))) unsigned char xs[];  // R x K activations
@@ -272,6 +273,36 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
   const uint32_t* we = w + (size_t)e * n * words_per_row;
   const uint16_t* se = scales + (size_t)e * n * G;
   const uint16_t* be = biases + (size_t)e * n * G;
+
+  // 0. Index validation, spread over the grid: workgroup b checks rows
+  //    b * GX_THREADS + tid (+ multiples of the grid's threads).  A row with
+  //    an expert index past the experts or an activation index past X is
+  //    zeroed here (no workgroup stores it: no expert matches the first, the
+  //    second's expert skips it) and counted, as is every descent of a
+  //    sorted routing.  The first row's indices are loaded now and checked
+  //    when the workgroup is done, so the loads never wait.
+  const int ck_stride = gridDim.x * gridDim.y * GX_THREADS;
+  const int ck_r0 = (blockIdx.y * gridDim.x + blockIdx.x) * GX_THREADS + tid;
+  uint32_t ck_re = 0u, ck_le = 0u, ck_next = 0xffffffffu;
+  if (ck_r0 < n_rows) {
+    ck_re = rhs[ck_r0];
+    ck_le = lhs ? lhs[ck_r0] : 0u;
+    if (sorted && ck_r0 + 1 < n_rows) ck_next = rhs[ck_r0 + 1];
+  }
+  auto check_rows = [&]() {
+    for (int r = ck_r0; r < n_rows; r += ck_stride) {
+      uint32_t re = ck_re, le = ck_le, nx = ck_next;
+      if (r != ck_r0) {
+        re = rhs[r];
+        le = lhs ? lhs[r] : 0u;
+        nx = sorted && r + 1 < n_rows ? rhs[r + 1] : 0xffffffffu;
+      }
+      const bool bad = re >= gridDim.y || (lhs && le >= (uint32_t)x_rows);
+      if (bad)
+        for (int j = 0; j < n; ++j) y[(size_t)r * n + j] = 0;
+      if (bad || (sorted && re > nx)) atomicAdd(status, 1u);
+    }
+  };
 
   // 1. Rows routed to e.
   const int nblk = (n_rows + 63) >> 6;
@@ -307,7 +338,10 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
   }
   __syncthreads();
   const int total = sh.total;
-  if (total == 0) return;  // uniform
+  if (total == 0) {  // uniform
+    check_rows();
+    return;
+  }
 
   // Wave w's slabs: 16-column slabs w, w+8, ... of the chunk.  Their first
   // GX_PF weight steps are requested now, so the stream is in flight while
@@ -450,12 +484,13 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
     }
     __syncthreads();  // LDS rows / activations are rewritten by the next pass
   }
+  check_rows();
 }
 
 template <typename TT, int BITS, int MB, int QS, int GSQ>
 hipError_t launch_q(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
                     const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
-                    int gs_shift, int n_chunks, int nc, int sb_vec) {
+                    int gs_shift, int n_chunks, int nc, int sb_vec, unsigned int* status) {
   static const hipError_t attr = [] {
     const void* fn = reinterpret_cast<const void*>(&gather_expert_kernel<TT, BITS, MB, QS, GSQ>);
     hipFuncAttributes fa;
@@ -469,7 +504,7 @@ hipError_t launch_q(hipStream_t s, const QuantArgs& q, const void* x, int x_rows
   hipLaunchKernelGGL((gather_expert_kernel<TT, BITS, MB, QS, GSQ>), dim3((unsigned)n_chunks, (unsigned)n_experts),
                      dim3(GX_THREADS), lds, s, q.w, static_cast<const uint16_t*>(q.scales),
                      static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x), x_rows, lhs,
-                     rhs, n_rows, static_cast<uint16_t*>(y), n, k, gs_shift, (int)sorted, nc, sb_vec);
+                     rhs, n_rows, static_cast<uint16_t*>(y), n, k, gs_shift, (int)sorted, nc, sb_vec, status);
   return hipGetLastError();
 }
 
@@ -480,7 +515,7 @@ hipError_t launch_q(hipStream_t s, const QuantArgs& q, const void* x, int x_rows
 template <typename TT, int BITS, int MB>
 hipError_t launch_mb(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
                      const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
-                     int gs_shift, int n_chunks, int nc) {
+                     int gs_shift, int n_chunks, int nc, unsigned int* status) {
   const int G = k / q.gs, units = k / 128;
   const uintptr_t al = reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases);
   // Vote runs start at (e n + c0) G entries, c0 a multiple of 128.
@@ -488,7 +523,7 @@ hipError_t launch_mb(hipStream_t s, const QuantArgs& q, const void* x, int x_row
   static const int forced = env_int("CPQ_GATHER_QS", 0);
 #define CPQ_GXQ(QS, GSQ)                                                                                  \
   return launch_q<TT, BITS, MB, QS, GSQ>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted,   \
-                                         gs_shift, n_chunks, nc, sb_vec)
+                                         gs_shift, n_chunks, nc, sb_vec, status)
   if (forced != 1) {
     if (q.gs == 64 && units % 4 == 0 && al % 16 == 0 && forced != 2) CPQ_GXQ(4, 64);
     if (q.gs == 64 && units % 2 == 0 && al % 8 == 0) CPQ_GXQ(2, 64);
@@ -501,7 +536,7 @@ hipError_t launch_mb(hipStream_t s, const QuantArgs& q, const void* x, int x_row
 template <typename TT, int BITS>
 hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
                     const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
-                    int cu_count) {
+                    int cu_count, unsigned int* status) {
   int gs_shift = 0;
   while ((1 << gs_shift) < q.gs) ++gs_shift;
   // Column chunks (whole multiples of 8 slabs = 128 columns): the count that
@@ -521,12 +556,12 @@ hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, int x_rows
   const int n_chunks = (n + nc - 1) / nc;
   if ((size_t)64 * k * 2 <= (size_t)GX_XBYTES)
     return launch_mb<TT, BITS, 4>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, gs_shift,
-                                  n_chunks, nc);
+                                  n_chunks, nc, status);
   if ((size_t)32 * k * 2 <= (size_t)GX_XBYTES)
     return launch_mb<TT, BITS, 2>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, gs_shift,
-                                  n_chunks, nc);
+                                  n_chunks, nc, status);
   return launch_mb<TT, BITS, 1>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, gs_shift,
-                                n_chunks, nc);
+                                n_chunks, nc, status);
 }
 
 }  // namespace
@@ -539,11 +574,12 @@ bool gather_expert_supported(int bits, int n_rows, int k) {
 
 hipError_t launch_gather_expert(hipStream_t s, const QuantArgs& q, const void* x, int x_rows,
                                 const uint32_t* lhs, const uint32_t* rhs, int n_rows, void* y,
-                                int n_experts, int n, int k, bool sorted, int cu_count) {
+                                int n_experts, int n, int k, bool sorted, int cu_count,
+                                unsigned int* status) {
 #define CPQ_GX(TT)                                                                                        \
   switch (q.bits) {                                                                                       \
-    case 4: return launch_t<TT, 4>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, cu_count); \
-    case 8: return launch_t<TT, 8>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, cu_count); \
+    case 4: return launch_t<TT, 4>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, cu_count, status); \
+    case 8: return launch_t<TT, 8>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, cu_count, status); \
     default: return hipErrorInvalidValue;                                                                 \
   }
   if (q.dtype == CPQ_DTYPE_BF16) { CPQ_GX(BF16) }

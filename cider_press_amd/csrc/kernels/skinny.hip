@@ -455,12 +455,7 @@ hipError_t launch_gather_t(hipStream_t s, const QuantArgs& q, const void* x, int
                            int n_experts, int n, int k, bool sorted, unsigned int* status) {
   if (n_rows == 0) return hipSuccess;
   const int gs_shift = shift_of(q.gs);
-  hipLaunchKernelGGL((gather_check_kernel<TT>), dim3((n_rows + 255) / 256), dim3(256), 0, s, lhs,
-                     rhs, n_rows, x_rows, n_experts, (int)sorted, static_cast<uint16_t*>(y), n,
-                     status);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  if (gather_expert_supported(BITS, n_rows, k)) {
+  if (gather_expert_supported(BITS, n_rows, k)) {  // validates the indices itself
     static const int cus = [] {
       int dev = 0, cu = 0;
       if (hipGetDevice(&dev) != hipSuccess ||
@@ -468,8 +463,13 @@ hipError_t launch_gather_t(hipStream_t s, const QuantArgs& q, const void* x, int
         cu = 256;
       return cu;
     }();
-    return launch_gather_expert(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, cus);
+    return launch_gather_expert(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, cus, status);
   }
+  hipLaunchKernelGGL((gather_check_kernel<TT>), dim3((n_rows + 255) / 256), dim3(256), 0, s, lhs,
+                     rhs, n_rows, x_rows, n_experts, (int)sorted, static_cast<uint16_t*>(y), n,
+                     status);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((gather_kernel<TT, BITS>), dim3((unsigned)((n + 15) / 16), (unsigned)n_experts),
                      dim3(256), slab_consts_bytes(k, q.gs), s, q.w, static_cast<const uint16_t*>(q.scales),
                      static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x),

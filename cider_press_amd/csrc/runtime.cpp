@@ -271,7 +271,8 @@ cpq_status cpq_commands_wait(cpq_commands* cmds) {
     std::string msg;
     if (bad[0])
       msg = "affine_gather_qmm: " + std::to_string(bad[0]) +
-            " row(s) carried an out-of-range lhs/rhs index; those rows were written as 0";
+            " row(s) carried an out-of-range lhs/rhs index (written as 0) or broke the ascending order "
+            "promised by sorted_indices";
     if (bad[1])
       msg += std::string(msg.empty() ? "" : "; ") + "embed_tokens: " + std::to_string(bad[1]) +
              " id(s) at or past the vocabulary size; those rows were written as 0";

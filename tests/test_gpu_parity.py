@@ -489,6 +489,46 @@ def test_gather_out_of_range_index_reported(device, library, oracle):
     cmds.commit_and_wait()  # the status word was cleared by the failed wait
 
 
+@pytest.mark.parametrize("k,gs", [(256, 64), (160, 32)])  # expert-major kernel / per-slab kernel
+def test_gather_index_validation_many_rows(device, library, oracle, k, gs):
+    """Bad expert and activation indices spread over 1500 rows (checked by
+    several workgroups): those rows are zeroed and counted, the others are
+    exact; a sorted routing with one descent is reported once."""
+    rng = np.random.default_rng(k)
+    e, n, rows, xr = 4, 48, 1500, 50
+    w_q, s, b = _experts(rng, e, n, k, gs, 4, "bf16")
+    x = make_x(rng, xr, k, "bf16")
+    rhs = rng.integers(0, e, size=rows).astype(np.uint32)
+    lhs = rng.integers(0, xr, size=rows).astype(np.uint32)
+    rhs[[0, 700]] = [e, 99]
+    lhs[[5, 1499]] = [xr, 0xFFFFFFFF]
+    bad = np.array([0, 5, 700, 1499])
+    X = device.upload(x.reshape(-1), "bf16")
+    W, S, B = _upload_weight(device, w_q, s, b, "bf16")
+    L, R = device.upload(lhs, "u32"), device.upload(rhs, "u32")
+    Y = device.upload(np.full(rows * n, 0x3F80, np.uint16), "bf16")
+    cmds = device.commands()
+    kg.affine_gather_qmm(cmds, library, X, W, S, B, L, R, Y, rows, n, k, e, gs, 4, x_rows=xr)
+    with pytest.raises(_lib.InvalidArgument, match="affine_gather_qmm: 4 row"):
+        cmds.commit_and_wait()
+    y = Y.to_numpy().reshape(rows, n)
+    assert not y[bad].any()
+    ok = np.setdiff1d(np.arange(rows), bad)
+    ref = oracle.gather_qmm_ref(x, lhs[ok], rhs[ok], w_q, s, b, len(ok), n, k, gs, 4, "bf16")
+    assert_tol(oracle, y[ok], ref, x, k, "bf16", "gather valid rows")
+
+    srt = np.sort(rng.integers(0, e, size=rows)).astype(np.uint32)
+    i = int(np.flatnonzero(srt[:-1] < srt[1:])[0])
+    srt[i], srt[i + 1] = srt[i + 1], srt[i]  # exactly one descent
+    R2 = device.upload(srt, "u32")
+    L2 = device.upload(rng.integers(0, xr, size=rows).astype(np.uint32), "u32")
+    kg.affine_gather_qmm(cmds, library, X, W, S, B, L2, R2, Y, rows, n, k, e, gs, 4, sorted_indices=True,
+                         x_rows=xr)
+    with pytest.raises(_lib.InvalidArgument, match="affine_gather_qmm: 1 row"):
+        cmds.commit_and_wait()
+    cmds.commit_and_wait()
+
+
 # ---------------------------------------------------------------------------
 # Runtime node (QuantizedWeight / Tensor.quantized_matmul / eval)
 # ---------------------------------------------------------------------------
