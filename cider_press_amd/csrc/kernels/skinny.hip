@@ -142,13 +142,13 @@ __device__ __forceinline__ bool slab_consts_store(const uint16_t* __restrict__ s
 // addresses and use zero constants (exact zero weights).  The slab constants
 // are loaded first, the weight prefetch issued behind them, and only then
 // staged to LDS.  All 64 * WAVES threads must call it (contains barriers).
-template <int BITS, int MB>
+template <int BITS, int MB, int NS>
 struct SkinnyGeom {
-  const uint32_t* wrow;
+  const uint32_t* wrow[NS];
   const uint16_t* xr[MB];
-  const f32x4* gcol;
+  const f32x4* gcol[NS];
   int u0, nu, nsteps, chunks, g, gs_shift;
-  bool col_ok;
+  bool col_ok[NS];
   __device__ __forceinline__ int chunk_of(int j) const { return min(4 * (u0 + j) + g, chunks - 1); }
   __device__ __forceinline__ void load_x(int j, u32x4 (&dst)[MB][4]) const {
     const int c = chunk_of(j);
@@ -165,36 +165,44 @@ struct SkinnyGeom {
   }
 };
 
-template <typename TT, int BITS, int MB, bool FAST, int PF>
-__device__ __forceinline__ void skinny_stream(const SkinnyGeom<BITS, MB>& sg, uint32_t (&wbuf)[PF][BITS],
-                                              u32x4 (&xa)[2][MB][4], f32x4 (&acc)[MB]) {
+// NS slabs (16 columns each) share every activation slice a step loads.
+template <typename TT, int BITS, int MB, bool FAST, int PF, int NS>
+__device__ __forceinline__ void skinny_stream(const SkinnyGeom<BITS, MB, NS>& sg, uint32_t (&wbuf)[NS][PF][BITS],
+                                              u32x4 (&xa)[2][MB][4], f32x4 (&acc)[NS][MB]) {
   for (int base = 0; base < sg.nsteps; base += PF) {
 #pragma unroll
     for (int p = 0; p < PF; ++p) {
       const int j = base + p;
-      uint32_t cur[BITS];
+      uint32_t cur[NS][BITS];
 #pragma unroll
-      for (int i = 0; i < BITS; ++i) cur[i] = wbuf[p][i];
-      if (base + PF < sg.nsteps) load_chunk<BITS>(sg.wrow, (size_t)sg.chunk_of(j + PF), wbuf[p]);
+      for (int sl = 0; sl < NS; ++sl)
+#pragma unroll
+        for (int i = 0; i < BITS; ++i) cur[sl][i] = wbuf[sl][p][i];
+      if (base + PF < sg.nsteps)
+#pragma unroll
+        for (int sl = 0; sl < NS; ++sl) load_chunk<BITS>(sg.wrow[sl], (size_t)sg.chunk_of(j + PF), wbuf[sl][p]);
       if (j + 1 < sg.nsteps) sg.load_x(j + 1, xa[(p + 1) & 1]);
       const int c = 4 * (sg.u0 + j) + sg.g;
-      f32x4 gcv = sg.gcol[(min(c, sg.chunks - 1) << 5) >> sg.gs_shift];
-      if (j >= sg.nu || c >= sg.chunks || !sg.col_ok) gcv = f32x4{0.f, 0.f, 0.f, 0.f};
-      const float sf = gcv[0], bf = gcv[1], s16 = sf * 0.0625f;
-      u32x4 bop[4];
-      bop[0] = dequant_slice_nat<TT, BITS, FAST, 0>(cur, sf, s16, bf, gcv[2], gcv[3]);
-      bop[1] = dequant_slice_nat<TT, BITS, FAST, 1>(cur, sf, s16, bf, gcv[2], gcv[3]);
-      bop[2] = dequant_slice_nat<TT, BITS, FAST, 2>(cur, sf, s16, bf, gcv[2], gcv[3]);
-      bop[3] = dequant_slice_nat<TT, BITS, FAST, 3>(cur, sf, s16, bf, gcv[2], gcv[3]);
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
+      for (int sl = 0; sl < NS; ++sl) {
+        f32x4 gcv = sg.gcol[sl][(min(c, sg.chunks - 1) << 5) >> sg.gs_shift];
+        if (j >= sg.nu || c >= sg.chunks || !sg.col_ok[sl]) gcv = f32x4{0.f, 0.f, 0.f, 0.f};
+        const float sf = gcv[0], bf = gcv[1], s16 = sf * 0.0625f;
+        u32x4 bop[4];
+        bop[0] = dequant_slice_nat<TT, BITS, FAST, 0>(cur[sl], sf, s16, bf, gcv[2], gcv[3]);
+        bop[1] = dequant_slice_nat<TT, BITS, FAST, 1>(cur[sl], sf, s16, bf, gcv[2], gcv[3]);
+        bop[2] = dequant_slice_nat<TT, BITS, FAST, 2>(cur[sl], sf, s16, bf, gcv[2], gcv[3]);
+        bop[3] = dequant_slice_nat<TT, BITS, FAST, 3>(cur[sl], sf, s16, bf, gcv[2], gcv[3]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mb] = Mfma16<TT>::run(xa[p & 1][mb][i], bop[i], acc[mb]);
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[sl][mb] = Mfma16<TT>::run(xa[p & 1][mb][i], bop[i], acc[sl][mb]);
+      }
     }
   }
 }
 
-template <typename TT, int BITS, int MB, int WAVES, class SH>
+template <typename TT, int BITS, int MB, int WAVES, class SH, int NS = 1>
 __device__ __forceinline__ void skinny_tile(const uint32_t* __restrict__ w,
                                             const uint16_t* __restrict__ scales,
                                             const uint16_t* __restrict__ biases, int n, int k,
@@ -203,13 +211,11 @@ __device__ __forceinline__ void skinny_tile(const uint32_t* __restrict__ w,
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nl = lane & 15;
-  const int col = n0 + nl;
   const int G = k >> gs_shift, GP = G + 1;
   const bool vec = (G & 7) == 0 &&
                    ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(biases)) & 15u) == 0;
 
-  SkinnyGeom<BITS, MB> sg;
-  sg.col_ok = col < n;
+  SkinnyGeom<BITS, MB, NS> sg;
   sg.chunks = k >> 5;
   const int units = (sg.chunks + 3) >> 2;
   const int per = (units + WAVES - 1) / WAVES;
@@ -218,62 +224,79 @@ __device__ __forceinline__ void skinny_tile(const uint32_t* __restrict__ w,
   sg.nsteps = (max(sg.nu, 0) + PF - 1) / PF * PF;
   sg.g = lane >> 4;
   sg.gs_shift = gs_shift;
-  sg.wrow = w + (size_t)(sg.col_ok ? col : 0) * ((size_t)k * BITS / 32);
-  sg.gcol = gc + nl * GP;
+#pragma unroll
+  for (int sl = 0; sl < NS; ++sl) {
+    const int col = n0 + 16 * sl + nl;
+    sg.col_ok[sl] = col < n;
+    sg.wrow[sl] = w + (size_t)(sg.col_ok[sl] ? col : 0) * ((size_t)k * BITS / 32);
+    sg.gcol[sl] = gc + (16 * sl + nl) * GP;
+  }
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) sg.xr[mb] = sh.xrow[16 * mb + nl];
 
   // 1. Constants' loads, then the weight / activation prefetch behind them.
-  SlabConsts sc;
-  slab_consts_load<64 * WAVES>(scales, biases, n, G, n0, vec, sc);
-  uint32_t wbuf[PF][BITS];
+  SlabConsts sc[NS];
+#pragma unroll
+  for (int sl = 0; sl < NS; ++sl) slab_consts_load<64 * WAVES>(scales, biases, n, G, n0 + 16 * sl, vec, sc[sl]);
+  uint32_t wbuf[NS][PF][BITS];
   u32x4 xa[2][MB][4];
   if (sg.nsteps > 0) {
 #pragma unroll
-    for (int p = 0; p < PF; ++p) load_chunk<BITS>(sg.wrow, (size_t)sg.chunk_of(p), wbuf[p]);
+    for (int p = 0; p < PF; ++p)
+#pragma unroll
+      for (int sl = 0; sl < NS; ++sl) load_chunk<BITS>(sg.wrow[sl], (size_t)sg.chunk_of(p), wbuf[sl][p]);
     sg.load_x(0, xa[0]);
   }
-  // 2. Constants into LDS, vote.
-  const bool fast = slab_consts_store<TT, 64 * WAVES>(scales, biases, n, G, n0, vec, sc, gc, GP);
+  // 2. Constants into LDS, vote (slab 16 sl + c at gc[(16 sl + c) * GP + g]).
+  bool fast = true;
+#pragma unroll
+  for (int sl = 0; sl < NS; ++sl)
+    fast &= slab_consts_store<TT, 64 * WAVES>(scales, biases, n, G, n0 + 16 * sl, vec, sc[sl], gc + 16 * sl * GP, GP);
 
   // 3. Stream.
-  f32x4 acc[MB];
+  f32x4 acc[NS][MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int sl = 0; sl < NS; ++sl)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[sl][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   if (sg.nsteps > 0) {
     if constexpr (BITS == 4 || BITS == 8) {
       if (fast)
-        skinny_stream<TT, BITS, MB, true, PF>(sg, wbuf, xa, acc);
+        skinny_stream<TT, BITS, MB, true, PF, NS>(sg, wbuf, xa, acc);
       else
-        skinny_stream<TT, BITS, MB, false, PF>(sg, wbuf, xa, acc);
+        skinny_stream<TT, BITS, MB, false, PF, NS>(sg, wbuf, xa, acc);
     } else {
-      skinny_stream<TT, BITS, MB, false, PF>(sg, wbuf, xa, acc);
+      skinny_stream<TT, BITS, MB, false, PF, NS>(sg, wbuf, xa, acc);
     }
   }
 
-  // 4. Sum the K-partial tiles.
+  // 4. Sum the K-partial tiles, one slab at a time.
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
+  for (int sl = 0; sl < NS; ++sl) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sh.red[wave][mb][lane][i] = acc[mb][i];
-  }
-  __syncthreads();
-  // Each wave finishes MB/4 (at least one) of the 16-row blocks.
-  for (int mb = wave; mb < MB; mb += WAVES) {
+    for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float v = sh.red[0][mb][lane][i];
-#pragma unroll
-      for (int wv = 1; wv < WAVES; ++wv) v += sh.red[wv][mb][lane][i];
-      const int m = 16 * mb + 4 * sg.g + i;  // D row of element i in this lane
-      uint16_t* yr = sh.yrow[m];
-      if (yr && sg.col_ok) yr[col] = TT::from_f32(v);
+      for (int i = 0; i < 4; ++i) sh.red[wave][mb][lane][i] = acc[sl][mb][i];
     }
+    __syncthreads();
+    // Each wave finishes MB/4 (at least one) of the 16-row blocks.
+    const int col = n0 + 16 * sl + nl;
+    for (int mb = wave; mb < MB; mb += WAVES) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = sh.red[0][mb][lane][i];
+#pragma unroll
+        for (int wv = 1; wv < WAVES; ++wv) v += sh.red[wv][mb][lane][i];
+        const int m = 16 * mb + 4 * sg.g + i;  // D row of element i in this lane
+        uint16_t* yr = sh.yrow[m];
+        if (yr && sg.col_ok[sl]) yr[col] = TT::from_f32(v);
+      }
+    }
+    __syncthreads();
   }
-  __syncthreads();
 }
 
-template <typename TT, int BITS, int MB, int WAVES>
+template <typename TT, int BITS, int MB, int WAVES, int NS = 1>
 __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint32_t* __restrict__ w,
                                                      const uint16_t* __restrict__ scales,
                                                      const uint16_t* __restrict__ biases,
@@ -283,7 +306,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint32_t* __re
   __shared__ TileShared<WAVES, MB> sh;
   extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
   f32x4* gc = reinterpret_cast<f32x4*>(dyn);
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * 16 * NS;
   const int row0 = blockIdx.y * 16 * MB;
   if (threadIdx.x < 16 * MB) {
     const int r = row0 + threadIdx.x;
@@ -291,7 +314,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_kernel(const uint32_t* __re
     sh.yrow[threadIdx.x] = r < m ? y + (size_t)r * n : nullptr;
   }
   __syncthreads();
-  skinny_tile<TT, BITS, MB, WAVES>(w, scales, biases, n, k, gs_shift, n0, gc, sh);
+  skinny_tile<TT, BITS, MB, WAVES, TileShared<WAVES, MB>, NS>(w, scales, biases, n, k, gs_shift, n0, gc, sh);
 }
 
 // Routed experts: workgroup (16-column slab, expert e).  Rows routed to e are
@@ -418,6 +441,19 @@ int shift_of(int gs) {
 // Dynamic LDS of the slab constants: 16 columns x (K/gs + 1) f32x4.
 size_t slab_consts_bytes(int k, int gs) { return (size_t)16 * (k / gs + 1) * 16; }
 
+// Raises the kernel's dynamic-LDS limit to what the CU holds (once per kernel).
+template <typename TT, int BITS, int MB, int WAVES, int NS>
+hipError_t skinny_allow_lds() {
+  static const hipError_t e = [] {
+    const void* fn = reinterpret_cast<const void*>(&skinny_kernel<TT, BITS, MB, WAVES, NS>);
+    hipFuncAttributes fa;
+    hipError_t r = hipFuncGetAttributes(&fa, fn);
+    if (r != hipSuccess) return r;
+    return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(160 * 1024 - fa.sharedSizeBytes));
+  }();
+  return e;
+}
+
 template <typename TT, int BITS>
 hipError_t launch_skinny_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n,
                            int k) {
@@ -442,9 +478,28 @@ hipError_t launch_skinny_t(hipStream_t s, const QuantArgs& q, const void* x, voi
   } else if (mb <= 2) {
     if (eight) go(skinny_kernel<TT, BITS, 2, 8>, 8); else go(skinny_kernel<TT, BITS, 2, 4>, 4);
   } else {
-    // 64 activation rows: the activation slices dominate the L2 traffic and
-    // 4 waves measure faster than 8.
-    go(skinny_kernel<TT, BITS, 4, 4>, 4);
+    // 64 activation rows: the activation slices dominate the L2 traffic (every
+    // slab rereads all of X), so once two-slab workgroups still give every
+    // CU one (N >= 32 x CUs) a workgroup takes two slabs per activation load
+    // (M = 64, N = 8192: 38.0 -> 23.4 us; at N = 4096 half the CUs would
+    // idle: 19.3 vs 22.2 us).  4 waves measure faster than 8.
+    static const int two_slabs = env_int("CPQ_SKINNY_NS", 0);  // tuning hook: 1 or 2 slabs per workgroup
+    static const int cus = [] {
+      int dev = 0, cu = 0;
+      if (hipGetDevice(&dev) != hipSuccess ||
+          hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cu <= 0)
+        cu = 256;
+      return cu;
+    }();
+    const bool ns2 = two_slabs ? two_slabs == 2 : (n + 31) / 32 >= cus;
+    if (ns2 && 2 * lds + sizeof(TileShared<4, 4>) <= (size_t)160 * 1024) {
+      const hipError_t a = skinny_allow_lds<TT, BITS, 4, 4, 2>();
+      if (a != hipSuccess) return a;
+      hipLaunchKernelGGL((skinny_kernel<TT, BITS, 4, 4, 2>), dim3((unsigned)((n + 31) / 32), gy), dim3(256), 2 * lds,
+                         s, q.w, sc, bi, xx, yy, m, n, k, gs_shift);
+    } else {
+      go(skinny_kernel<TT, BITS, 4, 4>, 4);
+    }
   }
   return hipGetLastError();
 }

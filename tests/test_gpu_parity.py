@@ -249,7 +249,9 @@ def test_quantized_matmul_routes_all_m(device, library, oracle, m, bits, gs):
     (20, 8192, 1024, 8, 64),    # 2 row blocks, 4 waves
     (20, 4096, 2048, 4, 32),    # 2 row blocks, 8 waves
     (48, 4096, 1024, 4, 64),    # 4 row blocks (M <= 64 at N <= 8192)
-    (64, 8192, 512, 4, 128),
+    (64, 8192, 512, 4, 128),    # 33..64 rows with N >= 32 x CUs: two slabs per workgroup
+    (48, 8192, 256, 4, 64),     # two slabs, three row blocks
+    (36, 8192, 512, 8, 32),     # two slabs, 8-bit, a ragged row block
 ])
 def test_small_m_wave_counts(device, library, oracle, m, n, k, bits, gs):
     rng = np.random.default_rng(m + n + k)
