@@ -139,6 +139,10 @@ hipError_t launch_gather_qmm(hipStream_t s, const QuantArgs& q, const void* x, i
                              const uint32_t* lhs, const uint32_t* rhs, int n_rows, void* y,
                              int n_experts, int n, int k, bool sorted, unsigned int* status);
 
+// Whether the small-M kernel's per-slab constants fit in LDS at this K and
+// group size (16 columns x (K/gs + 1) x 16 bytes next to its static LDS).
+bool skinny_fits(int k, int gs);
+
 // Row-count threshold below which cpq_quantized_matmul uses the skinny kernel.
 int skinny_max_m(const QuantArgs& q, int n, int k);
 

@@ -470,13 +470,22 @@ hipError_t launch_skinny_t(hipStream_t s, const QuantArgs& q, const void* x, voi
   // SIMD streaming; otherwise 4.
   static const int forced = env_int("CPQ_SKINNY_WAVES", 0);
   const bool eight = forced ? forced == 8 : (size_t)gx * gy < 512;
-  auto go = [&](auto kern, int waves) {
+  // Slab constants past the default 64 KiB of dynamic LDS (long K, small
+  // groups) need the kernel's limit raised first.
+  auto go = [&](auto kern, int waves, hipError_t (*allow)()) -> hipError_t {
+    if (lds > (size_t)64 * 1024) {
+      const hipError_t a = allow();
+      if (a != hipSuccess) return a;
+    }
     hipLaunchKernelGGL(kern, dim3(gx, gy), dim3(64 * waves), lds, s, q.w, sc, bi, xx, yy, m, n, k, gs_shift);
+    return hipGetLastError();
   };
   if (mb <= 1) {
-    if (eight) go(skinny_kernel<TT, BITS, 1, 8>, 8); else go(skinny_kernel<TT, BITS, 1, 4>, 4);
+    return eight ? go(skinny_kernel<TT, BITS, 1, 8>, 8, &skinny_allow_lds<TT, BITS, 1, 8, 1>)
+                 : go(skinny_kernel<TT, BITS, 1, 4>, 4, &skinny_allow_lds<TT, BITS, 1, 4, 1>);
   } else if (mb <= 2) {
-    if (eight) go(skinny_kernel<TT, BITS, 2, 8>, 8); else go(skinny_kernel<TT, BITS, 2, 4>, 4);
+    return eight ? go(skinny_kernel<TT, BITS, 2, 8>, 8, &skinny_allow_lds<TT, BITS, 2, 8, 1>)
+                 : go(skinny_kernel<TT, BITS, 2, 4>, 4, &skinny_allow_lds<TT, BITS, 2, 4, 1>);
   } else {
     // 64 activation rows: the activation slices dominate the L2 traffic (every
     // slab rereads all of X), so once two-slab workgroups still give every
@@ -498,7 +507,7 @@ hipError_t launch_skinny_t(hipStream_t s, const QuantArgs& q, const void* x, voi
       hipLaunchKernelGGL((skinny_kernel<TT, BITS, 4, 4, 2>), dim3((unsigned)((n + 31) / 32), gy), dim3(256), 2 * lds,
                          s, q.w, sc, bi, xx, yy, m, n, k, gs_shift);
     } else {
-      go(skinny_kernel<TT, BITS, 4, 4>, 4);
+      return go(skinny_kernel<TT, BITS, 4, 4>, 4, &skinny_allow_lds<TT, BITS, 4, 4, 1>);
     }
   }
   return hipGetLastError();
@@ -525,8 +534,21 @@ hipError_t launch_gather_t(hipStream_t s, const QuantArgs& q, const void* x, int
                      status);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  const size_t lds = slab_consts_bytes(k, q.gs);
+  if (lds + sizeof(TileShared<4, kMaxMB>) > (size_t)160 * 1024) return hipErrorInvalidValue;
+  if (lds > (size_t)64 * 1024) {  // long K, small groups: raise the kernel's dynamic-LDS limit once
+    static const hipError_t a = [] {
+      const void* fn = reinterpret_cast<const void*>(&gather_kernel<TT, BITS>);
+      hipFuncAttributes fa;
+      hipError_t r = hipFuncGetAttributes(&fa, fn);
+      if (r != hipSuccess) return r;
+      return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)(160 * 1024 - fa.sharedSizeBytes));
+    }();
+    if (a != hipSuccess) return a;
+  }
   hipLaunchKernelGGL((gather_kernel<TT, BITS>), dim3((unsigned)((n + 15) / 16), (unsigned)n_experts),
-                     dim3(256), slab_consts_bytes(k, q.gs), s, q.w, static_cast<const uint16_t*>(q.scales),
+                     dim3(256), lds, s, q.w, static_cast<const uint16_t*>(q.scales),
                      static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x),
                      x_rows, lhs, rhs, n_rows, static_cast<uint16_t*>(y), n, k, gs_shift,
                      (int)sorted);
@@ -545,6 +567,10 @@ hipError_t launch_gather_t(hipStream_t s, const QuantArgs& q, const void* x, int
   }
 
 }  // namespace
+
+bool skinny_fits(int k, int gs) {
+  return gs > 0 && slab_consts_bytes(k, gs) + sizeof(TileShared<8, kMaxMB>) <= (size_t)160 * 1024;
+}
 
 hipError_t launch_qmm_skinny(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m,
                              int n, int k) {

@@ -28,10 +28,10 @@ bool kernel_available(cpq_dtype dtype, uint32_t group_size, uint32_t bits) {
 // wins; at 33..64 rows it wins while the prefill kernel's 128-wide tiles leave
 // most CUs idle (N <= 8192: measured 19.7 vs 26.5 us at M = 64, N = K = 4096)
 // and loses once N fills the chip (58 vs 31 us at N = 12288).
-// CPQ_SKINNY_MAX_M overrides it, read once per process.
+// CPQ_SKINNY_MAX_M overrides it, read once per process.  Shapes whose slab
+// constants do not fit in LDS (K / gs beyond ~2300) never take it.
 int skinny_max_m(const QuantArgs& q, int n, int k) {
-  (void)q;
-  (void)k;
+  if (!skinny_fits(k, (int)q.gs)) return 0;  // its slab constants would not fit in LDS
   static const int lim = [] {
     const char* e = std::getenv("CPQ_SKINNY_MAX_M");
     return e && *e ? std::atoi(e) : 0;

@@ -262,6 +262,33 @@ def test_small_m_wave_counts(device, library, oracle, m, n, k, bits, gs):
     assert_tol(oracle, y, ref, x, k, "bf16", f"small-M m={m} n={n}")
 
 
+@pytest.mark.parametrize("m,n,k,gs", [
+    (4, 256, 12288, 32),    # slab constants 98 KiB: past the default dynamic-LDS limit
+    (40, 128, 12288, 32),   # 64-row blocks at the same size
+    (3, 64, 40960, 32),     # constants would not fit in LDS: the prefill path takes it
+])
+def test_small_m_long_k(device, library, oracle, m, n, k, gs):
+    rng = np.random.default_rng(m + k)
+    w_q, s, b = make_weight(rng, n, k, gs, 4, "bf16")
+    x = make_x(rng, m, k, "bf16")
+    y = run_qmm(device, library, w_q, s, b, x, m, n, k, gs, 4, "bf16", routed=True)
+    ref = oracle.qmm_ref(x, w_q, s, b, m, n, k, gs, 4, "bf16")
+    assert_tol(oracle, y, ref, x, k, "bf16", f"small-M long K m={m} k={k}")
+
+
+def test_gather_per_slab_long_k(device, library, oracle):
+    """The per-slab routed kernel (K beyond the expert-major kernel's LDS) with
+    98 KiB of slab constants."""
+    rng = np.random.default_rng(12288)
+    e, n, k, gs, rows = 2, 64, 12288, 32, 10
+    w_q, s, b = _experts(rng, e, n, k, gs, 4, "bf16")
+    x = make_x(rng, rows, k, "bf16")
+    rhs = rng.integers(0, e, size=rows).astype(np.uint32)
+    y = run_gather(device, library, x, w_q, s, b, None, rhs, rows, n, k, e, gs, 4, "bf16", False)
+    ref = oracle.gather_qmm_ref(x, None, rhs, w_q, s, b, rows, n, k, gs, 4, "bf16")
+    assert_tol(oracle, y, ref, x, k, "bf16", "gather per-slab long K")
+
+
 # The 4-bit prefill path runs the wide-tile kernel (128 x 128 tiles, K split
 # over 1, 2 or 4 workgroups, partial tiles summed by the last to finish);
 # CPQ_QMM_SPLIT forces the split, CPQ_QMM_WIDE=0 the earlier staged kernel.
