@@ -13,7 +13,7 @@
 // for the MFMA reads), and then streams the chunk's weights:
 //   - wave w owns the 16-column slabs w, w+8, ... of the chunk; for each slab
 //     it walks K in steps of 4 chunks (lane l: column l%16, chunk 4u + l/16),
-//     8 steps of weights and their (scale, bias) in flight;
+//     4 steps of weights and their (scale, bias) in flight;
 //   - each step is dequantized in registers (natural k order; the exact
 //     single-FMA form when every lane's group allows it, else fmaf) into four
 //     v_mfma_f32_16x16x32 B operands and multiplied against the MB 16-row
@@ -34,7 +34,7 @@ using namespace dev;
 
 constexpr int GX_WAVES = 8;
 constexpr int GX_THREADS = 64 * GX_WAVES;
-constexpr int GX_PF = 8;                   // steps in flight per wave
+constexpr int GX_PF = 4;                   // steps in flight per wave (4 measured ~2 % faster than 8, 12 slower)
 constexpr int GX_XBYTES = 128 * 1024;      // LDS for the staged activation rows
 constexpr int GX_MAXBLK = 1024;            // 64-row routing blocks (n_rows <= 65536)
 
