@@ -73,11 +73,42 @@ def make_copies(dev, rng, copies, n, k, gs, bits, dtype):
     return out, host0
 
 
+class Flusher:
+    """Evicts the 256 MB Infinity Cache (and L2) before a timed region with a
+    plain read of a 512 MiB buffer nothing else touches.  It reads, so it
+    leaves clean lines: a flush that wrote would have its dirty lines written
+    back to HBM during the timed region.  Without it the first weight copies
+    of the timed replay could still be cache-resident from the untimed one."""
+
+    def __init__(self, dev):
+        import ctypes
+
+        self.buf = dev.alloc_buffer(128 << 20, "u32")
+        self.sink = dev.alloc_buffer(1, "u32")
+        self.ptrs = (ctypes.c_void_p * 1)(self.buf.ptr)
+        self.lens = (ctypes.c_size_t * 1)(self.buf.byte_len)
+
+    def flush(self, cmds):
+        import ctypes
+
+        from cider_press_amd import _lib
+
+        _lib.check(_lib.lib().cpq_stream_read(cmds.handle, self.ptrs, self.lens, 1, ctypes.c_void_p(self.sink.ptr),
+                                              4096))
+
+
+_FLUSHER = None
+
+
 def time_graph(dev, steps, warmup, encode_step):
     """Capture `steps` calls in a graph, replay once untimed per warmup batch,
-    then time one replay between HIP events on the launch stream."""
+    replay the timed graph once untimed, flush the caches, then time one
+    replay between HIP events on the launch stream."""
+    global _FLUSHER
     from cider_press_amd.kernels import Event
 
+    if _FLUSHER is None:
+        _FLUSHER = Flusher(dev)
     cmds = dev.commands()
     if warmup:
         cmds.begin_capture()
@@ -91,6 +122,7 @@ def time_graph(dev, steps, warmup, encode_step):
         encode_step(cmds, i)
     g = cmds.end_capture()
     g.launch(cmds)          # one untimed replay of the timed graph itself
+    _FLUSHER.flush(cmds)    # no weight copy starts the timed replay cache-resident
     cmds.commit_and_wait()
     e0, e1 = Event(), Event()
     cmds.commit_and_wait()  # barrier: nothing in flight before the timed region
@@ -99,6 +131,31 @@ def time_graph(dev, steps, warmup, encode_step):
     e1.record(cmds)
     cmds.commit_and_wait()
     return e0.elapsed_ms(e1) / steps
+
+
+def parity_entry(rep, rows=None):
+    """The tolerance report as the line carries it: raw and beyond-rounding
+    errors with their bounds (max-abs is judged beyond the output's own
+    rounding to T; see oracle.tolerance_report)."""
+    out = {"ok": rep["ok"], "rel_l2": rep["rel_l2"], "rel_l2_bound": rep["rel_l2_bound"],
+           "max_abs": rep["max_abs"], "max_abs_beyond_rounding": rep["max_abs_beyond_rounding"],
+           "max_abs_bound": rep["max_abs_bound"]}
+    if rows is not None:
+        out["rows_checked"] = rows
+    return out
+
+
+def check_rows(m):
+    """Rows the oracle checks for an M-row prefill: all of them up to 512,
+    else two whole 128-row tiles plus every 7th row (every position inside a
+    tile is covered)."""
+    if m <= 512:
+        return np.arange(m)
+    rows = set(range(0, 128)) | set(range(m - 128, m)) | set(range(0, m, 7))
+    return np.array(sorted(rows))
+
+
+ORACLE_THREADS = min(16, os.cpu_count() or 1)
 
 
 def bench_qmv(dev, lib, args, rng):
@@ -122,14 +179,13 @@ def bench_qmv(dev, lib, args, rng):
         cmds = dev.commands()
         step(cmds, 0)
         cmds.commit_and_wait()
-        ref = O.qmm_ref(x, *host0, 1, n, k, gs, bits, dtype)
-        rep = O.tolerance_report(Y.to_numpy().reshape(1, n), ref, x, k, dtype)
-        parity = {"rel_l2": rep["rel_l2"], "max_abs": rep["max_abs"], "ok": rep["ok"]}
+        ref = O.qmm_ref(x, *host0, 1, n, k, gs, bits, dtype, threads=ORACLE_THREADS)
+        parity = parity_entry(O.tolerance_report(Y.to_numpy().reshape(1, n), ref, x, k, dtype))
     ms = time_graph(dev, args.steps, args.warmup, step)
     nbytes = algo_bytes(1, n, k, gs, bits)
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"ms": ms, "gbs": gbs, "bytes": nbytes, "parity": parity, "host0": host0, "x": x,
-            "shape": (n, k, gs, bits)}
+            "shape": (n, k, gs, bits), "copies": copies, "X": X}
 
 
 def bench_qmm(dev, lib, args, rng):
@@ -153,9 +209,8 @@ def bench_qmm(dev, lib, args, rng):
         cmds = dev.commands()
         step(cmds, 0)
         cmds.commit_and_wait()
-        ref = O.qmm_ref(x, *host0, m, n, k, gs, bits, dtype, threads=min(16, os.cpu_count() or 1))
-        rep = O.tolerance_report(Y.to_numpy().reshape(m, n), ref, x, k, dtype)
-        parity = {"rel_l2": rep["rel_l2"], "max_abs": rep["max_abs"], "ok": rep["ok"]}
+        ref = O.qmm_ref(x, *host0, m, n, k, gs, bits, dtype, threads=ORACLE_THREADS)
+        parity = parity_entry(O.tolerance_report(Y.to_numpy().reshape(m, n), ref, x, k, dtype))
     ms = time_graph(dev, args.qmm_steps, args.warmup, step)
     flops = 2.0 * m * n * k
     tflops = flops / (ms * 1e-3) / 1e12
@@ -164,14 +219,17 @@ def bench_qmm(dev, lib, args, rng):
 
 
 def _weights(dev, rng, copies, n, k, gs, bits, dtype, bias_noise=0.0):
+    """Rotated device copies and the host arrays of copy 0 (the parity input)."""
     from cider_press_amd.synthetic import make_weight
 
-    out = []
-    for _ in range(copies):
+    out, host0 = [], None
+    for c in range(copies):
         w, s, b = make_weight(rng, n, k, gs, bits, dtype, bias_noise=bias_noise)
+        if c == 0:
+            host0 = (w, s, b)
         out.append((dev.upload(w.reshape(-1), "u32"), dev.upload(s.reshape(-1), dtype),
                     dev.upload(b.reshape(-1), dtype)))
-    return out
+    return out, host0
 
 
 def _copies_for(nbytes, min_copies=2, working_set=600 << 20, cap=16):
@@ -184,39 +242,66 @@ def bench_configs(dev, lib, args, rng):
     """The remaining configurations of the measurement table: cfg1, cfg2b
     (decode), cfg3b/3c (prefill), cfg4 (small M through the routed op, all
     three quantizations), cfg5 (routed experts).  Same timing method as the
-    headline: rotated weight copies, one graph replay between HIP events."""
+    headline: rotated weight copies, one graph replay between HIP events.
+    Every configuration is also checked against the oracle (copy 0, one
+    eager call) unless --no-parity."""
     from cider_press_amd.kernels import gather as kg
     from cider_press_amd.kernels import qmm as kqmm
     from cider_press_amd.kernels import qmv as kqmv
     from cider_press_amd.synthetic import make_routing, make_x
 
+    O = None
+    if not args.no_parity:
+        from oracle import oracle as O  # checker only
+
     steps = args.config_steps
     res = {}
+
+    def eager(fn):
+        cmds = dev.commands()
+        fn(cmds)
+        cmds.commit_and_wait()
 
     def qmv_case(name, n, k, dtype, bias_noise=0.0):
         gs, bits = 64, 4
         wb = n * k // 2 + 4 * n * (k // gs)
-        cps = _weights(dev, rng, _copies_for(wb), n, k, gs, bits, dtype, bias_noise)
-        X = dev.upload(make_x(rng, 1, k, dtype).reshape(-1), dtype)
+        cps, h0 = _weights(dev, rng, _copies_for(wb), n, k, gs, bits, dtype, bias_noise)
+        x = make_x(rng, 1, k, dtype)
+        X = dev.upload(x.reshape(-1), dtype)
         Y = dev.alloc_buffer(n, dtype)
+        par = None
+        if O is not None:
+            eager(lambda c: kqmv.affine_qmv(c, lib, *cps[0], X, Y, k, gs, bits))
+            ref = O.qmm_ref(x, *h0, 1, n, k, gs, bits, dtype, threads=ORACLE_THREADS)
+            par = parity_entry(O.tolerance_report(Y.to_numpy().reshape(1, n), ref, x, k, dtype))
         ms = time_graph(dev, steps, args.warmup,
                         lambda c, i: kqmv.affine_qmv(c, lib, *cps[i % len(cps)], X, Y, k, gs, bits))
         nb = algo_bytes(1, n, k, gs, bits)
         res[name] = {"shape": f"x[1,{k}] . W[{n},{k}]^T 4b gs64 {dtype}", "us": round(ms * 1e3, 2),
                      "GB/s": round(nb / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                     "copies": len(cps)}
+                     "copies": len(cps), "parity": par}
 
     def qmm_case(name, m, n, k):
         gs, bits, dtype = 64, 4, "bf16"
         wb = n * k // 2 + 4 * n * (k // gs)
-        cps = _weights(dev, rng, _copies_for(wb), n, k, gs, bits, dtype)
-        X = dev.upload(make_x(rng, m, k, dtype).reshape(-1), dtype)
+        cps, h0 = _weights(dev, rng, _copies_for(wb), n, k, gs, bits, dtype)
+        x = make_x(rng, m, k, dtype)
+        X = dev.upload(x.reshape(-1), dtype)
         Y = dev.alloc_buffer(m * n, dtype)
+        par = None
+        if O is not None:
+            eager(lambda c: kqmm.affine_qmm_t(c, lib, *cps[0], X, Y, m, n, k, gs, bits))
+            rows = check_rows(m)
+            y = Y.to_numpy().reshape(m, n)
+            ref = O.qmm_ref(x[rows], *h0, len(rows), n, k, gs, bits, dtype, threads=ORACLE_THREADS)
+            par = parity_entry(O.tolerance_report(y[rows], ref, x[rows], k, dtype), rows=len(rows))
+            par["all_finite"] = bool(np.all(np.isfinite(O.bits_to_f32(y, dtype))))
         ms = time_graph(dev, max(10, steps // 4), args.warmup,
                         lambda c, i: kqmm.affine_qmm_t(c, lib, *cps[i % len(cps)], X, Y, m, n, k, gs, bits))
         tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
         res[name] = {"shape": f"X[{m},{k}] . W[{n},{k}]^T 4b gs64 bf16", "us": round(ms * 1e3, 2),
-                     "TFLOP/s": round(tf, 1), "mfma_frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 4), "copies": len(cps)}
+                     "TFLOP/s": round(tf, 1), "mfma_frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 4), "copies": len(cps),
+                     "parity": par}
 
     qmv_case("cfg1", 2048, 2048, "f16", bias_noise=1e-3)
     qmv_case("cfg2b", 4096, 12288, "bf16")
@@ -229,10 +314,16 @@ def bench_configs(dev, lib, args, rng):
     n = k = 4096
     for bits, gs in ((4, 64), (4, 32), (8, 64)):
         wb = n * k * bits // 8 + 4 * n * (k // gs)
-        cps = _weights(dev, rng, _copies_for(wb), n, k, gs, bits, "bf16")
+        cps, h0 = _weights(dev, rng, _copies_for(wb), n, k, gs, bits, "bf16")
         for m in (1, 4, 16, 64):
-            X = dev.upload(make_x(rng, m, k, "bf16").reshape(-1), "bf16")
+            x = make_x(rng, m, k, "bf16")
+            X = dev.upload(x.reshape(-1), "bf16")
             Y = dev.alloc_buffer(m * n, "bf16")
+            par = None
+            if O is not None:
+                eager(lambda c: kqmm.quantized_matmul(c, *cps[0], X, Y, m, n, k, gs, bits))
+                ref = O.qmm_ref(x, *h0, m, n, k, gs, bits, "bf16", threads=ORACLE_THREADS)
+                par = parity_entry(O.tolerance_report(Y.to_numpy().reshape(m, n), ref, x, k, "bf16"))
             ms = time_graph(dev, steps, args.warmup,
                             lambda c, i: kqmm.quantized_matmul(c, *cps[i % len(cps)], X, Y, m, n, k, gs, bits))
             nb = algo_bytes(m, n, k, gs, bits)
@@ -241,7 +332,8 @@ def bench_configs(dev, lib, args, rng):
                          "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
                          "hbm_frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                          "TFLOP/s": round(tf, 2), "mfma_frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 5),
-                         "kernel": "qmv" if m == 1 else ("small-M" if m <= (64 if n <= 8192 else 32) else "prefill")})
+                         "kernel": "qmv" if m == 1 else ("small-M" if m <= (64 if n <= 8192 else 32) else "prefill"),
+                         "parity": par})
         del cps
     res["cfg4"] = rows
 
@@ -254,52 +346,134 @@ def bench_configs(dev, lib, args, rng):
     for proj, (n, k) in (("up", (768, 2048)), ("down", (2048, 768))):
         gs, bits = 64, 4
         wb = e * (n * k // 2 + 4 * n * (k // gs))
-        cps = _weights(dev, rng, _copies_for(wb, cap=6), e * n, k, gs, bits, "bf16")
+        cps, h0 = _weights(dev, rng, _copies_for(wb, cap=6), e * n, k, gs, bits, "bf16")
         xin = make_x(rng, tokens if proj == "up" else tokens * topk, k, "bf16")
         X = dev.upload(xin.reshape(-1), "bf16")
         nrows = tokens * topk
         Y = dev.alloc_buffer(nrows * n, "bf16")
         for label, sorted_rows in (("unsorted", False), ("sorted", True)):
-            rhs = route[order] if sorted_rows else route
+            rhs = (route[order] if sorted_rows else route).astype(np.uint32)
             lh = lhs[order] if sorted_rows else lhs
             if proj == "down":
                 lh = None  # row r of the down projection reads its own hidden row
-            R = dev.upload(rhs.astype(np.uint32), "u32")
+            R = dev.upload(rhs, "u32")
             L = dev.upload(lh.astype(np.uint32), "u32") if lh is not None else None
-            ms = time_graph(dev, max(10, steps // 2), args.warmup,
-                            lambda c, i: kg.affine_gather_qmm(c, lib, X, *cps[i % len(cps)], L, R, Y, nrows, n, k, e,
-                                                              gs, bits, sorted_indices=sorted_rows,
-                                                              x_rows=xin.shape[0]))
+
+            def call(c, ws, L=L, R=R, sorted_rows=sorted_rows):
+                kg.affine_gather_qmm(c, lib, X, *ws, L, R, Y, nrows, n, k, e, gs, bits,
+                                     sorted_indices=sorted_rows, x_rows=xin.shape[0])
+
+            par = None
+            if O is not None:
+                eager(lambda c: call(c, cps[0]))
+                ref = O.gather_qmm_ref(xin, lh, rhs, *h0, nrows, n, k, gs, bits, "bf16", threads=ORACLE_THREADS)
+                par = parity_entry(O.tolerance_report(Y.to_numpy().reshape(nrows, n), ref, xin, k, "bf16"))
+            ms = time_graph(dev, max(10, steps // 2), args.warmup, lambda c, i: call(c, cps[i % len(cps)]))
             touched = len(np.unique(rhs))
             nb = touched * (n * k // 2 + 4 * n * (k // gs)) + nrows * k * 2 + nrows * n * 2
             tf = 2.0 * nrows * n * k / (ms * 1e-3) / 1e12
             res[f"cfg5_{proj}_{label}"] = {
                 "shape": f"{nrows} rows x {e} experts W[{n},{k}] 4b gs64 bf16", "us": round(ms * 1e3, 2),
                 "GB/s": round(nb / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                "TFLOP/s": round(tf, 2), "experts_touched": touched, "copies": len(cps)}
+                "TFLOP/s": round(tf, 2), "experts_touched": touched, "copies": len(cps), "parity": par}
         del cps
     return res
 
 
+def bench_ceiling(dev, args, rng, q=None):
+    """HBM ceiling of one launch over the qmv config 2a bytes: a plain
+    streaming read (cpq_stream_read) of the same kind of rotated copies
+    (W, scales, biases, x), timed by the same graph method as the decode
+    kernel.  Two grid sizes; the faster one is the ceiling."""
+    import ctypes
+
+    from cider_press_amd import _lib
+
+    n, k, gs, bits, dtype = 12288, 4096, 64, 4, "bf16"
+    if q is not None and q.get("copies"):
+        copies, X = q["copies"], q["X"]
+    else:
+        copies, _ = make_copies(dev, rng, args.copies, n, k, gs, bits, dtype)
+        from cider_press_amd.synthetic import make_x
+
+        X = dev.upload(make_x(rng, 1, k, dtype).reshape(-1), dtype)
+    sink = dev.alloc_buffer(1, "u32")
+    L = _lib.lib()
+    regs = []
+    for W, S, B in copies:
+        ptrs = (ctypes.c_void_p * 4)(W.ptr, S.ptr, B.ptr, X.ptr)
+        lens = (ctypes.c_size_t * 4)(W.byte_len, S.byte_len, B.byte_len, X.byte_len)
+        regs.append((ptrs, lens))
+    nbytes = sum(int(v) for v in regs[0][1])
+    out = {"what": "plain streaming read of the same rotated copies (W, scales, biases, x) in one launch per "
+                   "step, same graph method as the decode kernel", "bytes_read": nbytes, "grids": {}}
+    best = None
+    for nwg in (768, 2048):
+        def step(c, i, nwg=nwg):
+            ptrs, lens = regs[i % len(regs)]
+            _lib.check(L.cpq_stream_read(c.handle, ptrs, lens, 4, ctypes.c_void_p(sink.ptr), nwg))
+
+        ms = time_graph(dev, args.steps, args.warmup, step)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out["grids"][str(nwg)] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1)}
+        if best is None or gbs > best:
+            best = gbs
+    out["GB/s"] = round(best, 1)
+    out["frac_of_peak"] = round(best / HBM_PEAK_GBS, 4)
+    return out
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(q, budget_s):
-    """Oracle dequantize-and-dot (T-rounded weights, fp32 accumulate) on the host."""
+    """Oracle dequantize-and-dot (T-rounded weights, fp32 accumulate) on the
+    host: all-core and single-thread qmv GB/s at config 2a, and config 3a
+    GFLOP/s on a row sample.  Uses the AVX-512 build where the host has it."""
     from oracle import oracle as O
+    from cider_press_amd.synthetic import make_x
 
     n, k, gs, bits = q["shape"]
     w, s, b = q["host0"]
     threads = min(16, os.cpu_count() or 1)
-    O.cpu_baseline(q["x"], w, s, b, 1, n, k, gs, bits, "bf16", threads=threads)  # warm-up
-    reps, t0 = 0, time.perf_counter()
-    times = []
-    while time.perf_counter() - t0 < budget_s and reps < 10000:
-        t1 = time.perf_counter()
-        O.cpu_baseline(q["x"], w, s, b, 1, n, k, gs, bits, "bf16", threads=threads)
-        times.append(time.perf_counter() - t1)
-        reps += 1
-    med = float(np.median(times))
-    return {"value": round(q["bytes"] / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"qmv config 2a (N=12288, K=4096, 4-bit gs64, bf16), median of {reps} calls "
-                      f"over {budget_s:.0f} s, {threads} threads, oracle C dequantize-and-dot"}
+    isa = O.baseline_isa()
+
+    def timed(fn, seconds):
+        fn()  # warm-up
+        times, t0 = [], time.perf_counter()
+        while time.perf_counter() - t0 < seconds and len(times) < 10000:
+            t1 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t1)
+        return float(np.median(times)), len(times)
+
+    all_s, all_n = timed(lambda: O.cpu_baseline(q["x"], w, s, b, 1, n, k, gs, bits, "bf16", threads=threads),
+                         budget_s * 0.5)
+    one_s, one_n = timed(lambda: O.cpu_baseline(q["x"], w, s, b, 1, n, k, gs, bits, "bf16", threads=1),
+                         budget_s * 0.25)
+    # cfg3a (M=512, N=K=4096) on a sample of 32 activation rows x all 4096
+    # output rows of copy 0's first 4096 rows: 2*32*4096*4096 FLOP per call.
+    mq, nq = 32, 4096
+    xq = make_x(np.random.default_rng(1), mq, k, "bf16")
+    wq, sq, bq = w[:nq], s[:nq], b[:nq]
+    qmm_s, qmm_n = timed(lambda: O.cpu_baseline(xq, wq, sq, bq, mq, nq, k, gs, bits, "bf16", threads=threads),
+                         budget_s * 0.25)
+    return {"value": round(q["bytes"] / all_s / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"qmv config 2a (N=12288, K=4096, 4-bit gs64, bf16), median of {all_n} calls "
+                      f"over {budget_s * 0.5:.0f} s, {threads} threads, oracle C dequantize-and-dot ({isa})",
+            "nproc": os.cpu_count(), "cpu_model": _cpu_model(), "isa": isa,
+            "single_thread_GB/s": round(q["bytes"] / one_s / 1e9, 3), "single_thread_calls": one_n,
+            "qmm_cfg3a_GFLOP/s": round(2.0 * mq * nq * k / qmm_s / 1e9, 2),
+            "qmm_sample": f"config 3a shape on {mq} of its 512 activation rows (K=N=4096), median of {qmm_n} calls, "
+                          f"{threads} threads"}
 
 
 def bench_copy(args):
@@ -410,7 +584,7 @@ def main():
     ap.add_argument("--qmm-steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--copies", type=int, default=16)
-    ap.add_argument("--only", choices=["qmv", "qmm", "all", "copy", "configs"], default="all")
+    ap.add_argument("--only", choices=["qmv", "qmm", "all", "copy", "configs", "ceiling"], default="all")
     ap.add_argument("--no-configs", action="store_true", help="skip the cfg1/2b/3b/3c/4/5 table")
     ap.add_argument("--config-steps", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true")
@@ -452,6 +626,9 @@ def main():
                                    f"{args.copies} rotated weight copies", "device": info["name"],
                        "cu_count": info["cu_count"]}}
     q = None
+    if args.only == "ceiling":
+        print(json.dumps(bench_ceiling(dev, args, rng)), flush=True)
+        return
     if args.only in ("qmv", "all"):
         q = bench_qmv(dev, lib, args, rng)
         line["value"] = round(q["gbs"], 2)
@@ -460,6 +637,9 @@ def main():
                             "unit": "GB/s", "frac": round(q["gbs"] / HBM_PEAK_GBS, 4),
                             "traffic": load_traffic("qmv", QMV_KERNEL)}
         line["parity"] = {"qmv": q["parity"]}
+        c = bench_ceiling(dev, args, rng, q)
+        c["qmv_frac_of_ceiling"] = round(q["gbs"] / c["GB/s"], 4)
+        line["ceiling"] = c
     if args.only in ("qmm", "all"):
         r = bench_qmm(dev, lib, args, rng)
         line["qmm"] = {"workload": "config 3a: X[512,4096] . W[4096,4096]^T, 4-bit gs64, bf16",

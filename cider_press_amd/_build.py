@@ -32,6 +32,7 @@ SOURCES = [
     "kernels/qmm_n.hip",
     "kernels/gather.hip",
     "kernels/moe.hip",
+    "kernels/stream_read.hip",
 ]
 
 ARCH = "gfx950"

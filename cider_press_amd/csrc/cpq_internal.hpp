@@ -31,13 +31,13 @@ struct cpq_commands {
   // range, [2] MoE combine positions out of range)
   // add to it; cpq_commands_wait reads and clears it.
   unsigned int* status = nullptr;
-  // Split-K scratch of the prefill kernel: arrival counters (zero between
-  // launches) followed by fp32 partial tiles.  Grown only outside graph
-  // capture; replaced blocks stay allocated until the session is released,
-  // since a captured graph may still use them.
+  // Scratch of the split-K reductions and the routing sort: arrival
+  // counters (zero between launches) followed by fp32 partial tiles or sort
+  // histograms.  Allocated once when the session is made, with a fixed
+  // capacity; ops never grow it (kernel selection must not depend on graph
+  // capture, during which nothing can be allocated).
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
-  std::vector<void*> scratch_retired;
 };
 
 struct cpq_event {
@@ -108,6 +108,10 @@ hipError_t launch_qmm_skinny(hipStream_t s, const QuantArgs& q, const void* x, v
 hipError_t launch_qmm(cpq_commands* cmds, const QuantArgs& q, const void* x, void* y, int m, int n,
                       int k);
 
+// Prefill kernels that need no session scratch (staged, streaming or the
+// LDS-tiled fallback, by shape); any M, K, group size and width.
+hipError_t launch_qmm_unsplit(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k);
+
 // Wide-tile prefill kernel (4-bit, 128 x 128 tiles, optional split K).
 constexpr size_t kWideCounterBytes = 64 * 1024;  // arrival counters at the head of the scratch
 bool qmm_wide_fits(int m, int n, int k, int gs, int bits, int split);
@@ -119,10 +123,11 @@ hipError_t launch_qmm_wide(hipStream_t s, const QuantArgs& q, const void* x, voi
                            int k, int split, void* scratch);
 hipError_t zero_words(hipStream_t s, void* p, size_t n_words);
 
-// At least `bytes` of the session's split-K scratch (counters zeroed).
-// Fails with hipErrorStreamCaptureUnsupported when it would have to grow
-// while the stream is being captured.
-hipError_t session_scratch(cpq_commands* cmds, size_t bytes, void** out);
+// The session's scratch when it holds at least `bytes` (counters zeroed):
+// true and *out set, else false.  Depends on the session's fixed capacity
+// only, so a kernel choice made from it is the same eagerly and under graph
+// capture.
+bool session_scratch(const cpq_commands* cmds, size_t bytes, void** out);
 
 // Routed experts, expert-major kernel (4/8-bit, K % 128 == 0): one
 // workgroup per (expert, column chunk); it also validates the indices (bad
@@ -133,6 +138,10 @@ hipError_t launch_gather_expert(hipStream_t s, const QuantArgs& q, const void* x
                                 const uint32_t* lhs, const uint32_t* rhs, int n_rows, void* y,
                                 int n_experts, int n, int k, bool sorted, int cu_count,
                                 unsigned int* status);
+
+// Whether some routed-expert kernel takes this shape: the expert-major
+// kernel, or the per-slab kernel while its slab constants fit in LDS.
+bool gather_supported(int bits, int n_rows, int k, int gs);
 
 // Routed experts.
 hipError_t launch_gather_qmm(hipStream_t s, const QuantArgs& q, const void* x, int x_rows,
@@ -145,6 +154,10 @@ bool skinny_fits(int k, int gs);
 
 // Row-count threshold below which cpq_quantized_matmul uses the skinny kernel.
 int skinny_max_m(const QuantArgs& q, int n, int k);
+
+// Plain streaming read of up to 4 regions (measurement support).
+hipError_t launch_stream_read(hipStream_t s, const void* const* regions, const size_t* bytes, int n_regions,
+                              uint32_t* sink, int n_wg);
 
 // Integer from the environment (tuning and test hooks), dflt when unset.
 inline int env_int(const char* name, int dflt) {

@@ -832,27 +832,7 @@ hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, i
 
 }  // namespace
 
-// CPQ_QMM_WIDE=0 turns the wide-tile kernel off; CPQ_QMM_SPLIT=1|2|4 forces
-// its K split.  Both are read per call (test and tuning hooks).
-hipError_t launch_qmm(cpq_commands* cmds, const QuantArgs& q, const void* x, void* y, int m, int n,
-                      int k) {
-  hipStream_t s = cmds->stream;
-  const bool sb16 = ((reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases)) & 15u) == 0;
-  if (q.bits == 4 && sb16 && env_int("CPQ_QMM_WIDE", 1) != 0) {
-    const int forced = env_int("CPQ_QMM_SPLIT", 0);
-    int split = forced > 0 ? (qmm_wide_fits(m, n, k, q.gs, q.bits, forced) ? forced : 0)
-                           : qmm_wide_split(m, n, k, q.gs, q.bits, cmds->dev ? cmds->dev->cu_count : 0);
-    // A split needs session scratch; if it cannot grow (graph capture), try
-    // smaller splits.
-    for (; split > 1; split /= 2) {
-      if (!qmm_wide_fits(m, n, k, q.gs, q.bits, split)) continue;
-      void* scratch = nullptr;
-      if (session_scratch(cmds, qmm_wide_scratch_bytes(m, n, split), &scratch) == hipSuccess)
-        return launch_qmm_wide(s, q, x, y, m, n, k, split, scratch);
-    }
-    if (split == 1 && qmm_wide_fits(m, n, k, q.gs, q.bits, 1))
-      return launch_qmm_wide(s, q, x, y, m, n, k, 1, nullptr);
-  }
+hipError_t launch_qmm_unsplit(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k) {
 #define CPQ_QMM_BITS(TT)                                   \
   switch (q.bits) {                                        \
     case 2: return launch_t<TT, 2>(s, q, x, y, m, n, k);   \
@@ -867,6 +847,31 @@ hipError_t launch_qmm(cpq_commands* cmds, const QuantArgs& q, const void* x, voi
   if (q.dtype == CPQ_DTYPE_F16) { CPQ_QMM_BITS(F16) }
 #undef CPQ_QMM_BITS
   return hipErrorInvalidValue;
+}
+
+// CPQ_QMM_WIDE=0 turns the wide-tile kernel off; CPQ_QMM_SPLIT=1|2|4 forces
+// its K split.  Both are read per call (test and tuning hooks).
+hipError_t launch_qmm(cpq_commands* cmds, const QuantArgs& q, const void* x, void* y, int m, int n,
+                      int k) {
+  hipStream_t s = cmds->stream;
+  const bool sb16 = ((reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases)) & 15u) == 0;
+  if (q.bits == 4 && sb16 && env_int("CPQ_QMM_WIDE", 1) != 0) {
+    const int forced = env_int("CPQ_QMM_SPLIT", 0);
+    int split = forced > 0 ? (qmm_wide_fits(m, n, k, q.gs, q.bits, forced) ? forced : 0)
+                           : qmm_wide_split(m, n, k, q.gs, q.bits, cmds->dev ? cmds->dev->cu_count : 0);
+    // A split needs its partial tiles in the session's scratch; when they do
+    // not fit its fixed capacity, try smaller splits (a decision made from
+    // the shape and the session only, the same eagerly and under capture).
+    for (; split > 1; split /= 2) {
+      if (!qmm_wide_fits(m, n, k, q.gs, q.bits, split)) continue;
+      void* scratch = nullptr;
+      if (session_scratch(cmds, qmm_wide_scratch_bytes(m, n, split), &scratch))
+        return launch_qmm_wide(s, q, x, y, m, n, k, split, scratch);
+    }
+    if (split == 1 && qmm_wide_fits(m, n, k, q.gs, q.bits, 1))
+      return launch_qmm_wide(s, q, x, y, m, n, k, 1, nullptr);
+  }
+  return launch_qmm_unsplit(s, q, x, y, m, n, k);
 }
 
 }  // namespace cpq

@@ -562,8 +562,13 @@ hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, i
       }
     }
   }
-  if (lds > 160 * 1024)  // very long rows: the LDS-free small-M kernel
-    return launch_qmm_skinny(s, q, x, y, 1, n, k);
+  if (lds > 160 * 1024) {
+    // Very long rows: the small-M kernel while its slab constants fit in LDS
+    // (about 500 groups per row), beyond that a prefill kernel, which keeps
+    // no per-row constants in LDS.
+    if (skinny_fits(k, q.gs)) return launch_qmm_skinny(s, q, x, y, 1, n, k);
+    return launch_qmm_unsplit(s, q, x, y, 1, n, k);
+  }
   const int units = k / 128;
   if constexpr (BITS == 4) {
     // Few row blocks: split K over more waves to keep enough loads in flight.

@@ -529,13 +529,15 @@ hipError_t launch_gather_t(hipStream_t s, const QuantArgs& q, const void* x, int
     }();
     return launch_gather_expert(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, cus, status);
   }
+  // The shape must fit before anything is enqueued (the check kernel below
+  // writes y and the status word).
+  const size_t lds = slab_consts_bytes(k, q.gs);
+  if (lds + sizeof(TileShared<4, kMaxMB>) > (size_t)160 * 1024) return hipErrorInvalidValue;
   hipLaunchKernelGGL((gather_check_kernel<TT>), dim3((n_rows + 255) / 256), dim3(256), 0, s, lhs,
                      rhs, n_rows, x_rows, n_experts, (int)sorted, static_cast<uint16_t*>(y), n,
                      status);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const size_t lds = slab_consts_bytes(k, q.gs);
-  if (lds + sizeof(TileShared<4, kMaxMB>) > (size_t)160 * 1024) return hipErrorInvalidValue;
   if (lds > (size_t)64 * 1024) {  // long K, small groups: raise the kernel's dynamic-LDS limit once
     static const hipError_t a = [] {
       const void* fn = reinterpret_cast<const void*>(&gather_kernel<TT, BITS>);
@@ -570,6 +572,11 @@ hipError_t launch_gather_t(hipStream_t s, const QuantArgs& q, const void* x, int
 
 bool skinny_fits(int k, int gs) {
   return gs > 0 && slab_consts_bytes(k, gs) + sizeof(TileShared<8, kMaxMB>) <= (size_t)160 * 1024;
+}
+
+bool gather_supported(int bits, int n_rows, int k, int gs) {
+  return gather_expert_supported(bits, n_rows, k) ||
+         (gs > 0 && slab_consts_bytes(k, gs) + sizeof(TileShared<4, kMaxMB>) <= (size_t)160 * 1024);
 }
 
 hipError_t launch_qmm_skinny(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m,

@@ -29,7 +29,8 @@ bool kernel_available(cpq_dtype dtype, uint32_t group_size, uint32_t bits) {
 // most CUs idle (N <= 8192: measured 19.7 vs 26.5 us at M = 64, N = K = 4096)
 // and loses once N fills the chip (58 vs 31 us at N = 12288).
 // CPQ_SKINNY_MAX_M overrides it, read once per process.  Shapes whose slab
-// constants do not fit in LDS (K / gs beyond ~2300) never take it.
+// constants do not fit in LDS (K / gs beyond about 500 groups per row) never
+// take it.
 int skinny_max_m(const QuantArgs& q, int n, int k) {
   if (!skinny_fits(k, (int)q.gs)) return 0;  // its slab constants would not fit in LDS
   static const int lim = [] {
@@ -545,13 +546,14 @@ cpq_status cpq_affine_qmm_n(cpq_commands* cmds, cpq_dtype dtype, const uint32_t*
   if (st != CPQ_OK) return st;
   cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
   // Few output tiles: split K into fp32 partials in session scratch (past the
-  // prefill kernel's counters); without scratch (graph capture), no split.
+  // prefill kernel's counters) when the session's scratch holds them, else
+  // no split (the choice depends on the shape and the session only).
   int split = cpq::qmm_n_split((int)m, (int)n, (int)k, cmds->dev ? cmds->dev->cu_count : 0);
   float* partial = nullptr;
   if (split > 1) {
     void* scratch = nullptr;
     if (cpq::session_scratch(cmds, cpq::kWideCounterBytes + cpq::qmm_n_scratch_bytes((int)m, (int)n, split),
-                             &scratch) == hipSuccess)
+                             &scratch))
       partial = reinterpret_cast<float*>(static_cast<char*>(scratch) + cpq::kWideCounterBytes);
     else
       split = 1;
@@ -600,8 +602,11 @@ cpq_status cpq_moe_route(cpq_commands* cmds, cpq_dtype logits_dtype, const void*
     return fail(CPQ_ERR_INVALID_ARGUMENT, "moe_route: NULL buffer");
   void* scratch = nullptr;
   const size_t need = cpq::kWideCounterBytes + cpq::moe_sort_scratch_bytes((int)rows, (int)n_experts);
-  hipError_t e = cpq::session_scratch(cmds, need, &scratch);
-  if (e != hipSuccess) return cpq::hip_fail(e, "moe_route: session scratch");
+  if (!cpq::session_scratch(cmds, need, &scratch))
+    return fail(CPQ_ERR_BUFFER_TOO_LARGE, "moe_route: the sort needs " + std::to_string(need) +
+                                              " bytes of session scratch; the session holds " +
+                                              std::to_string(cmds->scratch_bytes) +
+                                              " (CPQ_SESSION_SCRATCH_MB sets it when the session is made)");
   // The scratch head holds the prefill kernel's arrival counters; the sort's
   // block histograms go after it.
   uint32_t* hist = reinterpret_cast<uint32_t*>(static_cast<char*>(scratch) + cpq::kWideCounterBytes);
@@ -654,11 +659,34 @@ cpq_status cpq_affine_gather_qmm(cpq_commands* cmds, cpq_dtype dtype, const void
   if (st != CPQ_OK) return st;
   if (x_rows == 0)
     return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_gather_qmm: x has no rows but lhs_indices select some");
+  if (!cpq::gather_supported((int)bits, (int)n_rows, (int)k, (int)group_size))
+    return fail(CPQ_ERR_INVALID_ARGUMENT,
+                "affine_gather_qmm: K=" + std::to_string(k) + " at group_size " + std::to_string(group_size) +
+                    " has " + std::to_string(k / group_size) +
+                    " groups per row: beyond what the per-slab routed kernel holds in LDS (about 600), and "
+                    "outside the expert-major kernel's shapes (4- or 8-bit, K % 128 == 0, bounded K and rows)");
   cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
   return cpq::launched(cpq::launch_gather_qmm(cmds->stream, q, x, (int)x_rows, lhs_indices,
                                               rhs_indices, (int)n_rows, y, (int)n_experts, (int)n,
                                               (int)k, sorted_indices != 0, cmds->status),
                        "affine_gather_qmm launch");
+}
+
+cpq_status cpq_stream_read(cpq_commands* cmds, const void* const* regions, const size_t* bytes, int n_regions,
+                           uint32_t* sink, int n_workgroups) {
+  if (!cmds) return fail(CPQ_ERR_INVALID_ARGUMENT, "stream_read: NULL command session");
+  if (n_regions < 1 || n_regions > 4 || !regions || !bytes)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "stream_read: 1..=4 regions with their lengths");
+  if (n_workgroups < 1 || n_workgroups > 65535)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "stream_read: n_workgroups outside 1..=65535");
+  if (!sink || (reinterpret_cast<uintptr_t>(sink) & 3u))
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "stream_read: sink must be a 4-byte aligned device pointer");
+  for (int g = 0; g < n_regions; ++g)
+    if ((bytes[g] && !regions[g]) || !cpq::aligned16(regions[g]) || bytes[g] % 16 != 0)
+      return fail(CPQ_ERR_INVALID_ARGUMENT, "stream_read: region " + std::to_string(g) +
+                                                " must be 16-byte aligned with a length that is a multiple of 16");
+  return cpq::launched(cpq::launch_stream_read(cmds->stream, regions, bytes, n_regions, sink, n_workgroups),
+                       "stream_read launch");
 }
 
 cpq_status cpq_quantized_matmul(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q,

@@ -32,33 +32,10 @@ cpq_status hip_fail(hipError_t e, const char* what) {
   return CPQ_ERR_HIP_API;
 }
 
-hipError_t session_scratch(cpq_commands* c, size_t bytes, void** out) {
-  if (bytes <= c->scratch_bytes) {
-    *out = c->scratch;
-    return hipSuccess;
-  }
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  hipError_t e = hipStreamIsCapturing(c->stream, &cs);
-  if (e != hipSuccess) return e;
-  if (cs != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
-  const size_t mib = size_t(1) << 20;
-  size_t want = std::max(bytes, 2 * c->scratch_bytes);
-  want = (want + mib - 1) / mib * mib;
-  void* p = nullptr;
-  e = hipMalloc(&p, want);
-  if (e != hipSuccess) return e;
-  // Counters start at zero; a kernel (not a memset) so the stream stays
-  // free of memset nodes should it be captured later.
-  e = zero_words(c->stream, p, kWideCounterBytes / 4);
-  if (e != hipSuccess) {
-    (void)hipFree(p);
-    return e;
-  }
-  if (c->scratch) c->scratch_retired.push_back(c->scratch);
-  c->scratch = p;
-  c->scratch_bytes = want;
-  *out = p;
-  return hipSuccess;
+bool session_scratch(const cpq_commands* c, size_t bytes, void** out) {
+  if (!c->scratch || bytes > c->scratch_bytes) return false;
+  *out = c->scratch;
+  return true;
 }
 
 }  // namespace cpq
@@ -215,15 +192,28 @@ static cpq_status make_commands(cpq_device* dev, hipStream_t stream, bool owns,
   c->stream = stream;
   c->owns_stream = owns;
   c->status = status;
-  // Split-K scratch for the prefill kernel, sized up front (CPQ_SESSION_SCRATCH_MB,
-  // default 64 MiB: 1024 partial tiles) so that a session whose first calls
-  // are captured into a graph still finds it.  Failure is not an error: the
-  // prefill path then runs unsplit.
+  // Scratch of the session's split-K reductions and routing sort, allocated
+  // here once with a fixed capacity (CPQ_SESSION_SCRATCH_MB, default 64 MiB:
+  // the arrival counters plus 1023 fp32 partial tiles of 128 x 128).  Ops
+  // never grow it, so the kernel an op selects depends on the shape and this
+  // capacity only -- never on whether the stream is being captured into a
+  // graph.  Without it (0, or the allocation failed) split-K kernels are not
+  // selected.
   const char* env = std::getenv("CPQ_SESSION_SCRATCH_MB");
   const long mb = env && *env ? std::atol(env) : 64;
   if (mb > 0) {
     void* p = nullptr;
-    (void)cpq::session_scratch(c, (size_t)mb << 20, &p);
+    if (hipMalloc(&p, (size_t)mb << 20) == hipSuccess) {
+      // Counters start at zero; a kernel (not a memset) keeps the stream free
+      // of memset nodes should it be captured later.
+      if (cpq::zero_words(stream, p, cpq::kWideCounterBytes / 4) == hipSuccess &&
+          hipStreamSynchronize(stream) == hipSuccess) {
+        c->scratch = p;
+        c->scratch_bytes = (size_t)mb << 20;
+      } else {
+        (void)hipFree(p);
+      }
+    }
     (void)hipGetLastError();
   }
   *out = c;
@@ -295,7 +285,6 @@ void cpq_commands_release(cpq_commands* cmds) {
   if (cmds->stream) (void)hipStreamSynchronize(cmds->stream);
   if (cmds->status) (void)hipFree(cmds->status);
   if (cmds->scratch) (void)hipFree(cmds->scratch);
-  for (void* p : cmds->scratch_retired) (void)hipFree(p);
   if (cmds->owns_stream && cmds->stream) (void)hipStreamDestroy(cmds->stream);
   delete cmds;
 }

@@ -130,6 +130,16 @@ cpq_status cpq_event_record(cpq_event* ev, cpq_commands* cmds);
 cpq_status cpq_event_elapsed_ms(cpq_event* start, cpq_event* end, float* out_ms);
 void cpq_event_release(cpq_event* ev);
 
+/* Streaming read of up to 4 device regions (16-byte aligned, lengths
+ * multiples of 16) in one launch of n_workgroups x 256 threads; `sink` (one
+ * device u32) is written only in the practically impossible case that the
+ * XOR of everything read equals a fixed 128-bit constant.  Measurement
+ * support: the HBM ceiling of one launch over a given byte count, timed
+ * beside the kernels it bounds.  No reference counterpart (its benches
+ * compare against the spec bandwidth, tests/qmv_dispatch_bench.rs:37-79). */
+cpq_status cpq_stream_read(cpq_commands* cmds, const void* const* regions, const size_t* bytes, int n_regions,
+                           uint32_t* sink, int n_workgroups);
+
 /* ------------------------------------------------------------------ */
 /* Quantization descriptor (runtime/src/quantization.rs:43-153)          */
 /* ------------------------------------------------------------------ */

@@ -209,9 +209,19 @@ static void* qmm_ref_worker(void* arg) {
       const double* xr = xd + mi * j->k;
       for (size_t r = r0; r < r1; ++r) {
         const float* wr = wd + (r - r0) * j->k;
-        double acc = 0.0;
-        for (size_t kk = 0; kk < j->k; ++kk) acc += xr[kk] * (double)wr[kk];
-        j->y[mi * j->n + r] = acc;
+        /* Four float64 partial sums (k mod 4) combined at the end: the
+         * products are exact in float64, and four independent chains keep
+         * the full-size references of the benchmark shapes affordable. */
+        double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+        size_t kk = 0;
+        for (; kk + 4 <= j->k; kk += 4) {
+          a0 += xr[kk] * (double)wr[kk];
+          a1 += xr[kk + 1] * (double)wr[kk + 1];
+          a2 += xr[kk + 2] * (double)wr[kk + 2];
+          a3 += xr[kk + 3] * (double)wr[kk + 3];
+        }
+        for (; kk < j->k; ++kk) a0 += xr[kk] * (double)wr[kk];
+        j->y[mi * j->n + r] = (a0 + a1) + (a2 + a3);
       }
     }
   }
@@ -255,12 +265,33 @@ void or_gather_qmm_ref(const uint16_t* x, const uint32_t* lhs, const uint32_t* r
                        int dtype, double* y, int threads) {
   size_t words_per_expert = n * k * (size_t)bits / 32u;
   size_t groups_per_expert = n * (k / (size_t)gs);
-  for (size_t r = 0; r < rows; ++r) {
-    size_t xr = lhs ? lhs[r] : r;
-    size_t e = rhs[r];
-    or_qmm_ref(x + xr * k, 1, w + e * words_per_expert, scales + e * groups_per_expert,
-               biases + e * groups_per_expert, n, k, gs, bits, dtype, y + r * n, threads);
+  /* Rows are grouped by expert so each expert is dequantized once: the rows
+   * of expert e are gathered into one activation block and reduced by
+   * or_qmm_ref (the per-element sums are the same as row by row). */
+  size_t* order = (size_t*)malloc((rows ? rows : 1) * sizeof(size_t));
+  uint16_t* xb = (uint16_t*)malloc((rows ? rows : 1) * k * sizeof(uint16_t));
+  double* yb = (double*)malloc((rows ? rows : 1) * n * sizeof(double));
+  uint8_t* done = (uint8_t*)calloc(rows ? rows : 1, 1);
+  for (size_t r0 = 0; r0 < rows; ++r0) {
+    if (done[r0]) continue;
+    const size_t e = rhs[r0];
+    size_t cnt = 0;
+    for (size_t r = r0; r < rows; ++r)
+      if (!done[r] && rhs[r] == e) {
+        order[cnt] = r;
+        done[r] = 1;
+        const size_t xr = lhs ? lhs[r] : r;
+        memcpy(xb + cnt * k, x + xr * k, k * sizeof(uint16_t));
+        ++cnt;
+      }
+    or_qmm_ref(xb, cnt, w + e * words_per_expert, scales + e * groups_per_expert,
+               biases + e * groups_per_expert, n, k, gs, bits, dtype, yb, threads);
+    for (size_t i = 0; i < cnt; ++i) memcpy(y + order[i] * n, yb + i * n, n * sizeof(double));
   }
+  free(order);
+  free(xb);
+  free(yb);
+  free(done);
 }
 
 /* ------------------------------------------------------------------ */

@@ -168,10 +168,42 @@ def qmv_mlx(x, w_q, scales, biases, m: int, n: int, k: int, gs: int, bits: int, 
     return y
 
 
+_AVX512_FLAGS = ("avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl")
+_base_lib = None
+
+
+def baseline_isa() -> str:
+    """"avx512" when the host CPU has the x86-64-v4 feature set, else "avx2"."""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+                    return "avx512" if all(f in flags for f in _AVX512_FLAGS) else "avx2"
+    except OSError:
+        pass
+    return "avx2"
+
+
+def _baseline_lib():
+    """The oracle build the CPU baseline runs: the AVX-512 twin on hosts with
+    AVX-512 (when built), else the portable AVX2 build."""
+    global _base_lib
+    if _base_lib is None:
+        path = os.path.join(HERE, "_build", "libcpq_oracle_avx512.so")
+        if baseline_isa() == "avx512" and os.path.exists(path):
+            L = ctypes.CDLL(path)
+            L.or_cpu_baseline.argtypes = [_u16p, _sz, _u32p, _u16p, _u16p, _sz, _sz, _i, _i, _i, _u16p, _i]
+            _base_lib = L
+        else:
+            _base_lib = lib()
+    return _base_lib
+
+
 def cpu_baseline(x, w_q, scales, biases, m: int, n: int, k: int, gs: int, bits: int, dtype: str,
                  threads=None) -> np.ndarray:
     y = np.empty((m, n), np.uint16)
-    lib().or_cpu_baseline(np.ascontiguousarray(x, np.uint16), m, np.ascontiguousarray(w_q, np.uint32),
+    _baseline_lib().or_cpu_baseline(np.ascontiguousarray(x, np.uint16), m, np.ascontiguousarray(w_q, np.uint32),
                           np.ascontiguousarray(scales, np.uint16), np.ascontiguousarray(biases, np.uint16),
                           n, k, gs, bits, _DT[dtype], y, _threads(threads))
     return y

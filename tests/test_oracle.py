@@ -308,7 +308,8 @@ MUTATIONS = {
     # wrong group index: element i reads the scale/bias of group (i+1)/gs
     "groupidx": ("size_t g = r * groups_per_row + i / (size_t)gs;", "size_t g = r * groups_per_row + (i + 1) / (size_t)gs;"),
     # last k term dropped from the reference matmul
-    "dropk": ("for (size_t kk = 0; kk < j->k; ++kk)", "for (size_t kk = 0; kk + 1 < j->k; ++kk)"),
+    "dropk": ("a3 += xr[kk + 3] * (double)wr[kk + 3];",
+              "a3 += (kk + 4 < j->k) ? xr[kk + 3] * (double)wr[kk + 3] : 0.0;"),
     # gather ignores the activation-row index
     "lhs": ("size_t xr = lhs ? lhs[r] : r;", "size_t xr = r;"),
 }
