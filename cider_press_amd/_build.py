@@ -23,6 +23,7 @@ SOURCES = [
     "ops.cpp",
     "graph.cpp",
     "safetensors.cpp",
+    "noalloc.hip",
     "kernels/dequantize.hip",
     "kernels/embed.hip",
     "kernels/qmv.hip",

@@ -148,6 +148,8 @@ SIGNATURES = {
     "cpq_affine_qmv": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _u32, _u32]),
     "cpq_affine_qmm_t": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz,
                                _u32, _u32]),
+    "cpq_affine_qmm_t_noalloc": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _sz, _sz, _sz,
+                                       _u32, _u32]),
     "cpq_affine_dequantize": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _u32, _u32]),
     "cpq_affine_gather_qmm": (_st, [_vp, _int, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _vp, _sz, _vp, _sz,
                                     _sz, _sz, _sz, _u32, _u32, _int]),

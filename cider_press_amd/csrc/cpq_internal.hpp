@@ -103,10 +103,24 @@ hipError_t launch_qmv(hipStream_t s, const QuantArgs& q, const void* x, void* y,
 hipError_t launch_qmm_skinny(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m,
                              int n, int k);
 
-// Prefill GEMM: LDS-tiled bf16/f16 MFMA with the W tile dequantized into LDS.
-// Uses the session's stream, and its split-K scratch when K is split.
-hipError_t launch_qmm(cpq_commands* cmds, const QuantArgs& q, const void* x, void* y, int m, int n,
-                      int k);
+// Prefill GEMM.  qmm_plan picks the kernel (and its K split) from the shape,
+// the CU count and the capacity of the scratch the caller can give it;
+// launch_qmm runs that plan, with `scratch` holding at least
+// plan.scratch_bytes (arrival counters zeroed) when that is nonzero.
+struct QmmPlan {
+  bool wide;             // the wide-tile kernel (else a kernel that needs no scratch)
+  int split;             // its K split
+  size_t scratch_bytes;  // scratch the plan uses (0: none)
+};
+QmmPlan qmm_plan(const QuantArgs& q, int m, int n, int k, int cu_count, size_t scratch_cap);
+hipError_t launch_qmm(hipStream_t s, const QmmPlan& plan, void* scratch, const QuantArgs& q, const void* x,
+                      void* y, int m, int n, int k);
+
+// qmm_plan + launch_qmm on a session (its stream, CU count and scratch).
+hipError_t launch_session_qmm(cpq_commands* cmds, const QuantArgs& q, const void* x, void* y, int m, int n, int k);
+
+// Capacity of a session's scratch when CPQ_SESSION_SCRATCH_MB is not set.
+constexpr size_t kDefaultSessionScratchBytes = size_t(64) << 20;
 
 // Prefill kernels that need no session scratch (staged, streaming or the
 // LDS-tiled fallback, by shape); any M, K, group size and width.

@@ -851,26 +851,28 @@ hipError_t launch_qmm_unsplit(hipStream_t s, const QuantArgs& q, const void* x, 
 
 // CPQ_QMM_WIDE=0 turns the wide-tile kernel off; CPQ_QMM_SPLIT=1|2|4 forces
 // its K split.  Both are read per call (test and tuning hooks).
-hipError_t launch_qmm(cpq_commands* cmds, const QuantArgs& q, const void* x, void* y, int m, int n,
-                      int k) {
-  hipStream_t s = cmds->stream;
+QmmPlan qmm_plan(const QuantArgs& q, int m, int n, int k, int cu_count, size_t scratch_cap) {
   const bool sb16 = ((reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases)) & 15u) == 0;
   if (q.bits == 4 && sb16 && env_int("CPQ_QMM_WIDE", 1) != 0) {
     const int forced = env_int("CPQ_QMM_SPLIT", 0);
     int split = forced > 0 ? (qmm_wide_fits(m, n, k, q.gs, q.bits, forced) ? forced : 0)
-                           : qmm_wide_split(m, n, k, q.gs, q.bits, cmds->dev ? cmds->dev->cu_count : 0);
-    // A split needs its partial tiles in the session's scratch; when they do
-    // not fit its fixed capacity, try smaller splits (a decision made from
-    // the shape and the session only, the same eagerly and under capture).
+                           : qmm_wide_split(m, n, k, q.gs, q.bits, cu_count);
+    // A split needs its partial tiles in scratch; when they do not fit the
+    // capacity, try smaller splits (a decision made from the shape and the
+    // capacity only, the same eagerly and under graph capture).
     for (; split > 1; split /= 2) {
       if (!qmm_wide_fits(m, n, k, q.gs, q.bits, split)) continue;
-      void* scratch = nullptr;
-      if (session_scratch(cmds, qmm_wide_scratch_bytes(m, n, split), &scratch))
-        return launch_qmm_wide(s, q, x, y, m, n, k, split, scratch);
+      const size_t need = qmm_wide_scratch_bytes(m, n, split);
+      if (need <= scratch_cap) return QmmPlan{true, split, need};
     }
-    if (split == 1 && qmm_wide_fits(m, n, k, q.gs, q.bits, 1))
-      return launch_qmm_wide(s, q, x, y, m, n, k, 1, nullptr);
+    if (split == 1 && qmm_wide_fits(m, n, k, q.gs, q.bits, 1)) return QmmPlan{true, 1, 0};
   }
+  return QmmPlan{false, 1, 0};
+}
+
+hipError_t launch_qmm(hipStream_t s, const QmmPlan& plan, void* scratch, const QuantArgs& q, const void* x,
+                      void* y, int m, int n, int k) {
+  if (plan.wide) return launch_qmm_wide(s, q, x, y, m, n, k, plan.split, plan.scratch_bytes ? scratch : nullptr);
   return launch_qmm_unsplit(s, q, x, y, m, n, k);
 }
 

@@ -62,6 +62,16 @@ cpq_status launched(hipError_t e, const char* what) {
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+// The prefill op on a session: its stream, CU count and fixed-capacity scratch.
+hipError_t launch_session_qmm(cpq_commands* cmds, const QuantArgs& q, const void* x, void* y, int m, int n, int k) {
+  const QmmPlan plan = qmm_plan(q, m, n, k, cmds->dev ? cmds->dev->cu_count : 0, cmds->scratch ? cmds->scratch_bytes : 0);
+  return launch_qmm(cmds->stream, plan, cmds->scratch, q, x, y, m, n, k);
+}
+
+namespace {
 bool aligned2(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1u) == 0; }
 
 cpq_status check_ptrs(const char* op, const void* w, const void* s, const void* b, const void* x,
@@ -382,8 +392,7 @@ cpq_status cpq_affine_qmm_t(cpq_commands* cmds, cpq_dtype dtype, const uint32_t*
   st = cpq::check_ptrs("affine_qmm_t", w_q, scales, biases, x, y);
   if (st != CPQ_OK) return st;
   cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
-  return cpq::launched(cpq::launch_qmm(cmds, q, x, y, (int)m, (int)n, (int)k),
-                       "affine_qmm_t launch");
+  return cpq::launched(cpq::launch_session_qmm(cmds, q, x, y, (int)m, (int)n, (int)k), "affine_qmm_t launch");
 }
 
 // ---------------------------------------------------------------------------
@@ -716,7 +725,7 @@ cpq_status cpq_quantized_matmul(cpq_commands* cmds, cpq_dtype dtype, const uint3
   if ((long)m <= cpq::skinny_max_m(q, (int)n, (int)k_physical))
     return cpq::launched(cpq::launch_qmm_skinny(cmds->stream, q, x, y, (int)m, (int)n, (int)k_physical),
                          "quantized_matmul (small-M) launch");
-  return cpq::launched(cpq::launch_qmm(cmds, q, x, y, (int)m, (int)n, (int)k_physical),
+  return cpq::launched(cpq::launch_session_qmm(cmds, q, x, y, (int)m, (int)n, (int)k_physical),
                        "quantized_matmul (prefill) launch");
 }
 

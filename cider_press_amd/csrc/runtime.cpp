@@ -200,7 +200,7 @@ static cpq_status make_commands(cpq_device* dev, hipStream_t stream, bool owns,
   // graph.  Without it (0, or the allocation failed) split-K kernels are not
   // selected.
   const char* env = std::getenv("CPQ_SESSION_SCRATCH_MB");
-  const long mb = env && *env ? std::atol(env) : 64;
+  const long mb = env && *env ? std::atol(env) : (long)(cpq::kDefaultSessionScratchBytes >> 20);
   if (mb > 0) {
     void* p = nullptr;
     if (hipMalloc(&p, (size_t)mb << 20) == hipSuccess) {

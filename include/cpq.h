@@ -180,6 +180,21 @@ cpq_status cpq_affine_qmm_t(cpq_commands* cmds, cpq_dtype dtype, const uint32_t*
                             void* y, size_t y_len, size_t m, size_t n, size_t k,
                             uint32_t group_size, uint32_t bits);
 
+/* affine_qmm_t for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, hosts that forbid allocation after
+ * start-up).  No counterpart in the reference.  Same validation, kernel
+ * choice and result as cpq_affine_qmm_t on a session with the default
+ * scratch capacity, enqueued on the caller's hipStream_t without a session.
+ * The split-K partial tiles and arrival counters live in a static device
+ * array of 16 MiB + 64 KiB per GPU, held until the process ends; a shape
+ * whose split needs more is refused with CPQ_ERR_BUFFER_TOO_LARGE before any
+ * launch.  It calls no allocator.  Calls that overlap on one GPU (two streams
+ * or threads) share that array and race: serialise them. */
+cpq_status cpq_affine_qmm_t_noalloc(void* hip_stream, cpq_dtype dtype, const uint32_t* w_q, size_t w_q_len,
+                                    const void* scales, size_t scales_len, const void* biases, size_t biases_len,
+                                    const void* x, size_t x_len, void* y, size_t y_len, size_t m, size_t n,
+                                    size_t k, uint32_t group_size, uint32_t bits);
+
 /* affine_dequantize_bf16_gs64_b4 (dequantize.rs:58-137), any (T, gs, bits):
  * out[i] = RNE_T(fmaf(scale, q_i, bias)) for out_len elements laid out as
  * consecutive groups of group_size.  out_len == 0 is a no-op. */
