@@ -107,8 +107,9 @@ hipError_t launch_qmm_skinny(hipStream_t s, const QuantArgs& q, const void* x, v
 // the CU count and the capacity of the scratch the caller can give it;
 // launch_qmm runs that plan, with `scratch` holding at least
 // plan.scratch_bytes (arrival counters zeroed) when that is nonzero.
+enum class QmmKernel { Unsplit, Wide, Dma };
 struct QmmPlan {
-  bool wide;             // the wide-tile kernel (else a kernel that needs no scratch)
+  QmmKernel kernel;      // Dma / Wide (4-bit, K split possible) or a kernel that needs no scratch
   int split;             // its K split
   size_t scratch_bytes;  // scratch the plan uses (0: none)
 };
@@ -136,6 +137,15 @@ size_t qmm_wide_scratch_bytes(int m, int n, int split);
 hipError_t launch_qmm_wide(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n,
                            int k, int split, void* scratch);
 hipError_t zero_words(hipStream_t s, void* p, size_t n_words);
+
+// Prefill kernel with two waves per SIMD (4-bit, 128 x 128 tiles, both
+// operands streamed into LDS, optional split K; same scratch layout as the
+// wide kernel: arrival counters, then fp32 partial tiles).
+bool qmm_dma_fits(int m, int n, int k, int gs, int bits, int split);
+int qmm_dma_split(int m, int n, int k, int gs, int bits, int cu_count);
+size_t qmm_dma_scratch_bytes(int m, int n, int split);
+hipError_t launch_qmm_dma(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k, int split,
+                          void* scratch);
 
 // The session's scratch when it holds at least `bytes` (counters zeroed):
 // true and *out set, else false.  Depends on the session's fixed capacity

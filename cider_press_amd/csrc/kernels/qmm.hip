@@ -853,6 +853,18 @@ hipError_t launch_qmm_unsplit(hipStream_t s, const QuantArgs& q, const void* x, 
 // its K split.  Both are read per call (test and tuning hooks).
 QmmPlan qmm_plan(const QuantArgs& q, int m, int n, int k, int cu_count, size_t scratch_cap) {
   const bool sb16 = ((reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases)) & 15u) == 0;
+  // CPQ_QMM_DMA=0 turns the two-waves-per-SIMD kernel off (tuning hook).
+  if (q.bits == 4 && sb16 && env_int("CPQ_QMM_DMA", 1) != 0) {
+    const int forced = env_int("CPQ_QMM_SPLIT", 0);
+    int split = forced > 0 ? (qmm_dma_fits(m, n, k, q.gs, q.bits, forced) ? forced : 0)
+                           : qmm_dma_split(m, n, k, q.gs, q.bits, cu_count);
+    for (; split > 1; split /= 2) {
+      if (!qmm_dma_fits(m, n, k, q.gs, q.bits, split)) continue;
+      const size_t need = qmm_dma_scratch_bytes(m, n, split);
+      if (need <= scratch_cap) return QmmPlan{QmmKernel::Dma, split, need};
+    }
+    if (split == 1 && qmm_dma_fits(m, n, k, q.gs, q.bits, 1)) return QmmPlan{QmmKernel::Dma, 1, 0};
+  }
   if (q.bits == 4 && sb16 && env_int("CPQ_QMM_WIDE", 1) != 0) {
     const int forced = env_int("CPQ_QMM_SPLIT", 0);
     int split = forced > 0 ? (qmm_wide_fits(m, n, k, q.gs, q.bits, forced) ? forced : 0)
@@ -863,16 +875,18 @@ QmmPlan qmm_plan(const QuantArgs& q, int m, int n, int k, int cu_count, size_t s
     for (; split > 1; split /= 2) {
       if (!qmm_wide_fits(m, n, k, q.gs, q.bits, split)) continue;
       const size_t need = qmm_wide_scratch_bytes(m, n, split);
-      if (need <= scratch_cap) return QmmPlan{true, split, need};
+      if (need <= scratch_cap) return QmmPlan{QmmKernel::Wide, split, need};
     }
-    if (split == 1 && qmm_wide_fits(m, n, k, q.gs, q.bits, 1)) return QmmPlan{true, 1, 0};
+    if (split == 1 && qmm_wide_fits(m, n, k, q.gs, q.bits, 1)) return QmmPlan{QmmKernel::Wide, 1, 0};
   }
-  return QmmPlan{false, 1, 0};
+  return QmmPlan{QmmKernel::Unsplit, 1, 0};
 }
 
 hipError_t launch_qmm(hipStream_t s, const QmmPlan& plan, void* scratch, const QuantArgs& q, const void* x,
                       void* y, int m, int n, int k) {
-  if (plan.wide) return launch_qmm_wide(s, q, x, y, m, n, k, plan.split, plan.scratch_bytes ? scratch : nullptr);
+  void* sp = plan.scratch_bytes ? scratch : nullptr;
+  if (plan.kernel == QmmKernel::Dma) return launch_qmm_dma(s, q, x, y, m, n, k, plan.split, sp);
+  if (plan.kernel == QmmKernel::Wide) return launch_qmm_wide(s, q, x, y, m, n, k, plan.split, sp);
   return launch_qmm_unsplit(s, q, x, y, m, n, k);
 }
 

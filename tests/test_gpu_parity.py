@@ -289,9 +289,21 @@ def test_gather_per_slab_long_k(device, library, oracle):
     assert_tol(oracle, y, ref, x, k, "bf16", "gather per-slab long K")
 
 
-# The 4-bit prefill path runs the wide-tile kernel (128 x 128 tiles, K split
-# over 1, 2 or 4 workgroups, partial tiles summed by the last to finish);
-# CPQ_QMM_SPLIT forces the split, CPQ_QMM_WIDE=0 the earlier staged kernel.
+# The 4-bit prefill path runs the two-waves-per-SIMD kernel ("dma": 128 x 128
+# tiles, both operands streamed into LDS, K split over 1, 2 or 4 workgroups,
+# partial tiles summed by the last to finish), else the one-wave wide-tile
+# kernel ("wide"), else the staged kernel.  CPQ_QMM_SPLIT forces the split,
+# CPQ_QMM_DMA=0 / CPQ_QMM_WIDE=0 turn the first two off.
+_KERNEL_ENV = {"dma": ("1", "1"), "wide": ("0", "1"), "staged": ("0", "0")}
+
+
+def _use_kernel(monkeypatch, kern):
+    dma, wide = _KERNEL_ENV[kern]
+    monkeypatch.setenv("CPQ_QMM_DMA", dma)
+    monkeypatch.setenv("CPQ_QMM_WIDE", wide)
+
+
+@pytest.mark.parametrize("kern", ["dma", "wide"])
 @pytest.mark.parametrize("m,n,k,gs,dtype,split", [
     (256, 512, 2048, 64, "bf16", 1),
     (256, 512, 2048, 64, "bf16", 2),
@@ -303,14 +315,15 @@ def test_gather_per_slab_long_k(device, library, oracle):
     (129, 256, 2048, 128, "bf16", 2),
     (64, 4096, 4096, 64, "bf16", 4),       # config 4 at M = 64
 ])
-def test_qmm_wide_parity(device, library, oracle, monkeypatch, m, n, k, gs, dtype, split):
+def test_qmm_wide_parity(device, library, oracle, monkeypatch, m, n, k, gs, dtype, split, kern):
+    _use_kernel(monkeypatch, kern)
     monkeypatch.setenv("CPQ_QMM_SPLIT", str(split))
     rng = np.random.default_rng(m + n + split)
     w_q, s, b = make_weight(rng, n, k, gs, 4, dtype)
     x = make_x(rng, m, k, dtype)
     y = run_qmm(device, library, w_q, s, b, x, m, n, k, gs, 4, dtype)
     ref = oracle.qmm_ref(x, w_q, s, b, m, n, k, gs, 4, dtype)
-    assert_tol(oracle, y, ref, x, k, dtype, f"wide split={split} {m}x{n}x{k}")
+    assert_tol(oracle, y, ref, x, k, dtype, f"{kern} split={split} {m}x{n}x{k}")
 
 
 # Scale / bias pairs outside the single-FMA fast path's exactness range: a
@@ -320,10 +333,13 @@ def test_qmm_wide_parity(device, library, oracle, monkeypatch, m, n, k, gs, dtyp
 _SLOW_SB = {"bf16": (0x3000, 0x3C23), "f16": (0x0001, 0x211F)}
 
 
+_KERNEL_SPLITS = [("dma", 2), ("dma", 1), ("wide", 2), ("wide", 1), ("staged", 1)]
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
-@pytest.mark.parametrize("wide,split", [(1, 2), (1, 1), (0, 1)])
-def test_qmm_mixed_fast_and_slow_tiles(device, library, oracle, monkeypatch, dtype, wide, split):
-    monkeypatch.setenv("CPQ_QMM_WIDE", str(wide))
+@pytest.mark.parametrize("kern,split", _KERNEL_SPLITS)
+def test_qmm_mixed_fast_and_slow_tiles(device, library, oracle, monkeypatch, dtype, kern, split):
+    _use_kernel(monkeypatch, kern)
     monkeypatch.setenv("CPQ_QMM_SPLIT", str(split))
     m, n, k, gs = 160, 384, 2048, 64
     rng = np.random.default_rng(5)
@@ -333,16 +349,16 @@ def test_qmm_mixed_fast_and_slow_tiles(device, library, oracle, monkeypatch, dty
     x = make_x(rng, m, k, dtype)
     y = run_qmm(device, library, w_q, s, b, x, m, n, k, gs, 4, dtype)
     ref = oracle.qmm_ref(x, w_q, s, b, m, n, k, gs, 4, dtype)
-    assert_tol(oracle, y, ref, x, k, dtype, f"mixed wide={wide} split={split}")
+    assert_tol(oracle, y, ref, x, k, dtype, f"mixed {kern} split={split}")
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
-@pytest.mark.parametrize("wide,split", [(1, 2), (1, 1), (0, 1)])
-def test_qmm_zero_scales_and_biases(device, library, oracle, monkeypatch, dtype, wide, split):
+@pytest.mark.parametrize("kern,split", _KERNEL_SPLITS)
+def test_qmm_zero_scales_and_biases(device, library, oracle, monkeypatch, dtype, kern, split):
     """Zero scales or biases fail the packed exponent check but pass the
     exact predicate, so their tiles stay on the fast dequantization; a -0
     bias under a negative scale does not (the fast path would give +0)."""
-    monkeypatch.setenv("CPQ_QMM_WIDE", str(wide))
+    _use_kernel(monkeypatch, kern)
     monkeypatch.setenv("CPQ_QMM_SPLIT", str(split))
     m, n, k, gs = 130, 384, 2048, 64
     rng = np.random.default_rng(9)
@@ -355,12 +371,14 @@ def test_qmm_zero_scales_and_biases(device, library, oracle, monkeypatch, dtype,
     x = make_x(rng, m, k, dtype)
     y = run_qmm(device, library, w_q, s, b, x, m, n, k, gs, 4, dtype)
     ref = oracle.qmm_ref(x, w_q, s, b, m, n, k, gs, 4, dtype)
-    assert_tol(oracle, y, ref, x, k, dtype, f"zeros wide={wide} split={split}")
+    assert_tol(oracle, y, ref, x, k, dtype, f"zeros {kern} split={split}")
 
 
-def test_qmm_wide_split_is_deterministic(device, library, oracle, monkeypatch):
+@pytest.mark.parametrize("kern", ["dma", "wide"])
+def test_qmm_wide_split_is_deterministic(device, library, oracle, monkeypatch, kern):
     """The split-K sum adds the parts in k order whatever order the
     workgroups finish in: repeated calls give identical bits."""
+    _use_kernel(monkeypatch, kern)
     monkeypatch.setenv("CPQ_QMM_SPLIT", "4")
     m, n, k, gs = 512, 1024, 4096, 64
     rng = np.random.default_rng(9)
