@@ -200,18 +200,26 @@ __device__ __forceinline__ int prev_slot(int ra) { return ra == 0 ? 2 * DASLOT :
 // Stage kinds: copies still to issue near the end of the K range.
 enum { ST_MAIN = 0, ST_LAST3 = 1, ST_LAST2 = 2, ST_LAST1 = 3 };
 
-// One stage.  bcur holds stage s's B operands (dequantized during stage
-// s-1); bnext receives stage s+1's.  Copies per stage and wave: A(s+2) x 4
-// then W(s+3) x 1 while those stages exist (the prologue issues W0, A0 x 4,
-// W1, A1 x 4, W2; stage S-3 issues only A(S-1); the last two issue
-// nothing).  So at the start of stage s "all but the younger copies" -- 5
-// for a main stage and for S-3, 4 for S-2, none for S-1 -- proves that A(s)
-// and W(s+1) landed for this wave; the barrier extends that to every wave
-// and frees the slots refilled next (A slot of stage s-1, W slot of stage s:
-// both read before this barrier).  Slots: A(s) and W(s) in slot s % 3.
-template <typename TT, bool FAST, int KIND>
-__device__ __forceinline__ void dma_stage(const DmaGeom& g, int s, int ra, const u32x4 (&bcur)[2][2],
-                                          u32x4 (&bnext)[2][2], f32x16 (&acc)[4][2]) {
+// One stage, skewed by half a stage: after stage s's barrier the wave first
+// runs stage s-1's second k step (its A fragments and B operands are in
+// registers already), which keeps the matrix cores busy while stage s's A
+// fragments arrive from LDS, then stage s's first k step; between them it
+// dequantizes stage s+1's B operands.
+//   acur <- A(s) fragments; aprev holds A(s-1) (k step 1 still to run);
+//   bcur holds B(s) (dequantized during stage s-1); bprev holds B(s-1);
+//   bprev is overwritten with B(s+1) once its k step 1 has been issued.
+// Copies per stage and wave: A(s+2) x 4 then W(s+3) x 1 while those stages
+// exist (the prologue issues W0, A0 x 4, W1, A1 x 4, W2; stage S-3 issues
+// only A(S-1); the last two issue nothing).  So at the start of stage s "all
+// but the younger copies" -- 5 for a main stage and for S-3, 4 for S-2,
+// none for S-1 -- proves that A(s) and W(s+1) landed for this wave; the
+// barrier extends that to every wave and frees the slots refilled next (A
+// slot of stage s-1 and W slot of stage s, both read before this barrier).
+template <typename TT, bool FAST, int KIND, bool PREV>
+__device__ __forceinline__ void dma_stage(const DmaGeom& g, int s, int ra, u32x4 (&acur)[4][2],
+                                          const u32x4 (&aprev)[4][2], const u32x4 (&bcur)[2][2],
+                                          u32x4 (&bprev)[2][2], f32x16 (&acc)[4][2]) {
+  __builtin_amdgcn_sched_barrier(0);
   asm volatile("" ::: "memory");
   if constexpr (KIND == ST_LAST1)
     wait_vm_lgkm<0>();
@@ -224,42 +232,61 @@ __device__ __forceinline__ void dma_stage(const DmaGeom& g, int s, int ra, const
   if constexpr (KIND == ST_MAIN || KIND == ST_LAST3) dma_a(g, s + 2, prev_slot(ra));
   if constexpr (KIND == ST_MAIN) dma_w(g, s + 3, ra >> 2);
   const unsigned char* aslot = g.smem + ra;
-  u32x4 a[4][2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int t = 0; t < 2; ++t) a[i][t] = *reinterpret_cast<const u32x4*>(aslot + g.a_off[t] + i * 8192);
-  if constexpr (KIND != ST_LAST1) dequant_stage<TT, FAST>(read_stage_w(g, s + 1, next_slot(ra) >> 2), bnext);
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
+    for (int i = 0; i < 4; ++i) acur[i][t] = *reinterpret_cast<const u32x4*>(aslot + g.a_off[t] + i * 8192);
+  StageW sw;
+  if constexpr (KIND != ST_LAST1) sw = read_stage_w(g, s + 1, next_slot(ra) >> 2);
+  if constexpr (PREV) {
+#pragma unroll
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i][cb] = mfma32<TT>(a[i][t], bcur[cb][t], acc[i][cb]);
+      for (int i = 0; i < 4; ++i) acc[i][cb] = mfma32<TT>(aprev[i][1], bprev[cb][1], acc[i][cb]);
+  }
+  if constexpr (KIND != ST_LAST1) dequant_stage<TT, FAST>(sw, bprev);
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i][cb] = mfma32<TT>(acur[i][0], bcur[cb][0], acc[i][cb]);
 }
 
-// S is even and at least 4: stages 0 .. S-5 in pairs, then S-4 (even), and
-// the last three with their own copy counts.
+// Stage S-1's second k step, after the loop.
+template <typename TT>
+__device__ __forceinline__ void dma_tail(const u32x4 (&alast)[4][2], const u32x4 (&blast)[2][2], f32x16 (&acc)[4][2]) {
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i][cb] = mfma32<TT>(alast[i][1], blast[cb][1], acc[i][cb]);
+}
+
+// S is even and at least 8: stage 0 (nothing before it), stages 1 .. S-5 in
+// pairs, then S-4 (even), and the last three with their own copy counts.
+// Even stages use (a0, b0) as current and (a1, b1) as previous; odd stages
+// the other way round.
 template <typename TT, bool FAST>
 __device__ __forceinline__ void dma_loop(const DmaGeom& g, f32x16 (&acc)[4][2]) {
   // Stage 0's operands: W0 and the constants are visible (prologue barrier).
-  u32x4 b0[2][2], b1[2][2];
+  u32x4 a0[4][2], a1[4][2], b0[2][2], b1[2][2];
   dequant_stage<TT, FAST>(read_stage_w(g, 0, 0), b0);
   int ra = 0;
-  int s = 0;
+  dma_stage<TT, FAST, ST_MAIN, false>(g, 0, ra, a0, a1, b0, b1, acc);
+  ra = next_slot(ra);
+  int s = 1;
   for (; s < g.S - 4; s += 2) {
-    dma_stage<TT, FAST, ST_MAIN>(g, s, ra, b0, b1, acc);
+    dma_stage<TT, FAST, ST_MAIN, true>(g, s, ra, a1, a0, b1, b0, acc);
     ra = next_slot(ra);
-    dma_stage<TT, FAST, ST_MAIN>(g, s + 1, ra, b1, b0, acc);
+    dma_stage<TT, FAST, ST_MAIN, true>(g, s + 1, ra, a0, a1, b0, b1, acc);
     ra = next_slot(ra);
   }
-  dma_stage<TT, FAST, ST_MAIN>(g, s, ra, b0, b1, acc);
+  // s == S-3 here (S even): stages S-3 (odd), S-2 (even), S-1 (odd).
+  dma_stage<TT, FAST, ST_LAST3, true>(g, s, ra, a1, a0, b1, b0, acc);
   ra = next_slot(ra);
-  dma_stage<TT, FAST, ST_LAST3>(g, s + 1, ra, b1, b0, acc);
+  dma_stage<TT, FAST, ST_LAST2, true>(g, s + 1, ra, a0, a1, b0, b1, acc);
   ra = next_slot(ra);
-  dma_stage<TT, FAST, ST_LAST2>(g, s + 2, ra, b0, b1, acc);
-  ra = next_slot(ra);
-  dma_stage<TT, FAST, ST_LAST1>(g, s + 3, ra, b1, b0, acc);
+  dma_stage<TT, FAST, ST_LAST1, true>(g, s + 2, ra, a1, a0, b1, b0, acc);
+  dma_tail<TT>(a1, b1, acc);
 }
 
 template <typename TT>
