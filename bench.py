@@ -48,7 +48,7 @@ BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic.json")
 COPY_BYTES = 512 << 20         # calibration copy: 512 MiB read + 512 MiB written
 QMV_KERNEL = "qmv_lean_kernel<cpq::dev::BF16, 4"
-QMM_KERNEL = "qmm_wide_kernel<cpq::dev::BF16"
+QMM_KERNEL = "qmm_dma_kernel<cpq::dev::BF16"
 COPY_KERNEL = "copy"
 
 
@@ -495,15 +495,16 @@ def bench_copy(args):
 
 
 # Launch grids (threads) of the headline dispatches: qmv config 2a runs 768
-# workgroups of 256 threads, qmm config 3a 256 workgroups of 256 threads.  The
-# same kernels also serve the secondary configurations at other grids.
+# workgroups of 256 threads, qmm config 3a 256 workgroups of 512 threads (128
+# output tiles of 128 x 128, K split in two).  The same kernels also serve the
+# secondary configurations at other grids.
 QMV_GRID = 768 * 256
-QMM_GRID = 256 * 256
+QMM_GRID = 256 * 512
 
 
-def _pmc_per_dispatch(d, counter):
-    """Mean counter value (KiB) per dispatch, by (kernel name, grid size),
-    from rocprofv3 CSV output."""
+def _pmc_table(d):
+    """Mean value per dispatch of every counter in a rocprofv3 --pmc run, by
+    (kernel name, grid size): {counter: {(kernel, grid): (mean, dispatches)}}."""
     import csv
     import glob
 
@@ -511,10 +512,35 @@ def _pmc_per_dispatch(d, counter):
     for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
         with open(f) as fh:
             for r in csv.DictReader(fh):
-                if r["Counter_Name"] != counter:
-                    continue
-                acc.setdefault((r["Kernel_Name"], int(r["Grid_Size"])), []).append(float(r["Counter_Value"]))
-    return {k: (sum(v) / len(v), len(v)) for k, v in acc.items()}
+                key = (r["Kernel_Name"], int(r["Grid_Size"]))
+                acc.setdefault(r["Counter_Name"], {}).setdefault(key, []).append(float(r["Counter_Value"]))
+    return {c: {k: (sum(v) / len(v), len(v)) for k, v in t.items()} for c, t in acc.items()}
+
+
+def _pmc_per_dispatch(d, counter):
+    """Mean counter value (KiB) per dispatch, by (kernel name, grid size),
+    from rocprofv3 CSV output."""
+    return _pmc_table(d).get(counter, {})
+
+
+def counter_summary(dirs, min_dispatches=20):
+    """Markdown table of every counter of one or more --pmc runs, mean per
+    dispatch, one row per (kernel, grid) seen in every run with at least
+    `min_dispatches` dispatches (the benchmark's timed kernels, not set-up)."""
+    tabs = {}
+    for d in dirs:
+        tabs.update(_pmc_table(d))
+    keys = None
+    for t in tabs.values():
+        ks = {k for k, (_, n) in t.items() if n >= min_dispatches}
+        keys = ks if keys is None else keys & ks
+    cols = sorted(tabs)
+    print("| kernel | grid | dispatches | " + " | ".join(cols) + " |")
+    print("|---|---:|---:|" + "---:|" * len(cols))
+    for k in sorted(keys or (), key=lambda kk: (kk[0], kk[1])):
+        n = min(tabs[c][k][1] for c in cols)
+        vals = " | ".join(f"{tabs[c][k][0]:.6g}" for c in cols)
+        print(f"| `{k[0]}` | {k[1]} | {n} | {vals} |")
 
 
 def trace_summary(d):
@@ -592,7 +618,12 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"))
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_DIR")
+    ap.add_argument("--counter-summary", nargs="+", metavar="PMC_DIR")
     args = ap.parse_args()
+
+    if args.counter_summary:
+        counter_summary(args.counter_summary)
+        return
 
     if args.trace_summary:
         trace_summary(args.trace_summary)
