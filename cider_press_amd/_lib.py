@@ -136,6 +136,17 @@ SIGNATURES = {
     "cpq_commands_end_capture": (_st, [_vp, _pp]),
     "cpq_graph_launch": (_st, [_vp, _vp]),
     "cpq_graph_release": (None, [_vp]),
+    "cpq_commands_record_input": (_st, [_vp, _c.c_uint64]),
+    "cpq_commands_record_output": (_st, [_vp, _c.c_uint64]),
+    "cpq_commands_record_unresolved_input": (_st, [_vp]),
+    "cpq_commands_elide_next_barrier": (_st, [_vp]),
+    "cpq_device_supports_stage_boundary_sampling": (_int, [_vp]),
+    "cpq_device_gpu_timestamp_period_ns": (_st, [_vp, _c.POINTER(_c.c_double)]),
+    "cpq_commands_create_profiled": (_st, [_vp, _sz, _pp]),
+    "cpq_commands_begin_profiled_op": (_st, [_vp, _c.c_char_p]),
+    "cpq_commands_profiled_info": (_st, [_vp, _psz, _psz]),
+    "cpq_commands_commit_wait_resolve": (_st, [_vp, _vp, _sz, _psz]),
+    "cpq_completion_result": (_st, [_int]),
     "cpq_event_create": (_st, [_pp]),
     "cpq_event_record": (_st, [_vp, _vp]),
     "cpq_event_elapsed_ms": (_st, [_vp, _vp, _c.POINTER(_c.c_float)]),

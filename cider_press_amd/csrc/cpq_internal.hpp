@@ -38,6 +38,22 @@ struct cpq_commands {
   // capture, during which nothing can be allocated).
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
+  // Per-op GPU timing of a profiled session (cpq_commands_create_profiled):
+  // two timing events per op of capacity, created with the session; the
+  // index of the next unused one; per recorded op its label and the indices
+  // of its start and end events; whether the last op is still open (its end
+  // not yet recorded).  Empty for an ordinary session.
+  struct ProfiledOp {
+    std::string label;
+    size_t start = 0, end = 0;
+  };
+  bool profiled = false;
+  std::vector<hipEvent_t> prof_events;
+  size_t prof_cursor = 0;
+  std::vector<ProfiledOp> prof_ops;
+  bool prof_open = false;
+  // Labels of the last resolved batch; cpq_gpu_segment.label points here.
+  std::vector<std::string> prof_resolved_labels;
 };
 
 struct cpq_event {

@@ -159,6 +159,16 @@ cpq_status cpq_qweight_from_bytes(cpq_device* dev, cpq_dtype dtype, size_t n, si
     return fail(CPQ_ERR_INVALID_ARGUMENT, "QuantizedWeight: k_logical=" + std::to_string(k_logical) +
                                               " must be a multiple of group_size=" +
                                               std::to_string(group_size));
+  // Per-row packing (quantized.rs:146-163): K itself, not only N*K, must hold
+  // whole groups and whole u32 words.
+  if (k_physical % group_size != 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "QuantizedWeight: inner dim K=" + std::to_string(k_physical) +
+                                              " must be a multiple of group_size=" + std::to_string(group_size) +
+                                              " (per-row groups must divide evenly)");
+  if ((k_physical * bits) % 32 != 0)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "QuantizedWeight: K*bits=" + std::to_string(k_physical * bits) +
+                                              " must be a multiple of 32 (per-row packed u32 words must divide "
+                                              "evenly)");
   size_t words = 0, groups = 0;
   if (n > SIZE_MAX / k_physical)
     return fail(CPQ_ERR_INVALID_ARGUMENT, "QuantizedWeight: N*K overflows usize");

@@ -248,10 +248,7 @@ cpq_status cpq_commands_commit(cpq_commands* cmds) {
 cpq_status cpq_commands_wait(cpq_commands* cmds) {
   if (!cmds) return fail(CPQ_ERR_INVALID_ARGUMENT, "cpq_commands_wait: NULL session");
   hipError_t e = hipStreamSynchronize(cmds->stream);
-  if (e != hipSuccess)
-    return fail(CPQ_ERR_COMMAND_BUFFER_FAILED,
-                std::string("GPU command stream failed: ") + hipGetErrorName(e) + " (" +
-                    hipGetErrorString(e) + ")");
+  if (e != hipSuccess) return cpq_completion_result((int)e);
   unsigned int bad[3] = {0u, 0u, 0u};
   e = hipMemcpy(bad, cmds->status, sizeof(bad), hipMemcpyDeviceToHost);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpy(status word)");
@@ -283,10 +280,149 @@ cpq_status cpq_commands_commit_and_wait(cpq_commands* cmds) {
 void cpq_commands_release(cpq_commands* cmds) {
   if (!cmds) return;
   if (cmds->stream) (void)hipStreamSynchronize(cmds->stream);
+  for (hipEvent_t ev : cmds->prof_events) (void)hipEventDestroy(ev);
   if (cmds->status) (void)hipFree(cmds->status);
   if (cmds->scratch) (void)hipFree(cmds->scratch);
   if (cmds->owns_stream && cmds->stream) (void)hipStreamDestroy(cmds->stream);
   delete cmds;
+}
+
+// ---------------------------------------------------------------------------
+// Encoder hazard hooks (commands.rs:139-153, 290-296).  One in-order stream
+// per session orders every launch after the previous one, so there is no
+// fence to wait or barrier to elide; the hooks only check the session.
+// ---------------------------------------------------------------------------
+
+cpq_status cpq_commands_record_input(cpq_commands* cmds, uint64_t) {
+  return cmds ? CPQ_OK : fail(CPQ_ERR_INVALID_ARGUMENT, "record_input: NULL session");
+}
+
+cpq_status cpq_commands_record_output(cpq_commands* cmds, uint64_t) {
+  return cmds ? CPQ_OK : fail(CPQ_ERR_INVALID_ARGUMENT, "record_output: NULL session");
+}
+
+cpq_status cpq_commands_record_unresolved_input(cpq_commands* cmds) {
+  return cmds ? CPQ_OK : fail(CPQ_ERR_INVALID_ARGUMENT, "record_unresolved_input: NULL session");
+}
+
+cpq_status cpq_commands_elide_next_barrier(cpq_commands* cmds) {
+  return cmds ? CPQ_OK : fail(CPQ_ERR_INVALID_ARGUMENT, "elide_next_barrier: NULL session");
+}
+
+// ---------------------------------------------------------------------------
+// Profiled sessions: per-op GPU windows from timing events on the session's
+// stream (GpuSampler, gpu_sampler.rs:44-162; commands.rs:155-181, 361-374).
+// ---------------------------------------------------------------------------
+
+int cpq_device_supports_stage_boundary_sampling(cpq_device* dev) { return dev ? 1 : 0; }
+
+cpq_status cpq_device_gpu_timestamp_period_ns(cpq_device* dev, double* out_ns_per_tick) {
+  if (!dev || !out_ns_per_tick)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "gpu_timestamp_period_ns: NULL argument");
+  *out_ns_per_tick = 1.0;  // segments are resolved to nanoseconds
+  return CPQ_OK;
+}
+
+cpq_status cpq_commands_create_profiled(cpq_device* dev, size_t op_capacity, cpq_commands** out) {
+  if (!dev || !out) return fail(CPQ_ERR_INVALID_ARGUMENT, "commands_profiled: NULL argument");
+  *out = nullptr;
+  if (op_capacity > SIZE_MAX / 2) return fail(CPQ_ERR_HIP_API, "GpuSampler: op_capacity * 2 overflow");
+  cpq_commands* c = nullptr;
+  cpq_status st = cpq_commands_create(dev, &c);
+  if (st != CPQ_OK) return st;
+  c->profiled = true;
+  c->prof_events.reserve(2 * op_capacity);
+  for (size_t i = 0; i < 2 * op_capacity; ++i) {
+    hipEvent_t ev = nullptr;
+    hipError_t e = hipEventCreate(&ev);
+    if (e != hipSuccess) {
+      cpq_commands_release(c);
+      return hip_fail(e, "GpuSampler: hipEventCreate");
+    }
+    c->prof_events.push_back(ev);
+  }
+  *out = c;
+  return CPQ_OK;
+}
+
+// Ends the open op's window: its end event follows everything encoded for it.
+static cpq_status close_profiled_op(cpq_commands* c) {
+  if (!c->prof_open) return CPQ_OK;
+  c->prof_open = false;
+  hipError_t e = hipEventRecord(c->prof_events[c->prof_ops.back().end], c->stream);
+  return e == hipSuccess ? CPQ_OK : hip_fail(e, "begin_profiled_op: hipEventRecord(end)");
+}
+
+cpq_status cpq_commands_begin_profiled_op(cpq_commands* cmds, const char* label) {
+  if (!cmds) return fail(CPQ_ERR_INVALID_ARGUMENT, "begin_profiled_op: NULL session");
+  if (!cmds->profiled) return CPQ_OK;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(cmds->stream, &cap);
+  if (e != hipSuccess) return hip_fail(e, "begin_profiled_op: hipStreamIsCapturing");
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "begin_profiled_op: the session's stream is being captured");
+  cpq_status st = close_profiled_op(cmds);
+  if (st != CPQ_OK) return st;
+  // Reserve a (start, end) pair; past capacity, stop timing further ops
+  // rather than failing mid-batch (gpu_sampler.rs reserve, commands.rs:172-180).
+  const size_t start = cmds->prof_cursor, end = start + 1;
+  if (end >= cmds->prof_events.size()) return CPQ_OK;
+  cmds->prof_cursor = end + 1;
+  cmds->prof_ops.push_back({label ? std::string(label) : std::string(), start, end});
+  e = hipEventRecord(cmds->prof_events[start], cmds->stream);
+  if (e != hipSuccess) {
+    cmds->prof_ops.pop_back();
+    cmds->prof_cursor = start;
+    return hip_fail(e, "begin_profiled_op: hipEventRecord(start)");
+  }
+  cmds->prof_open = true;
+  return CPQ_OK;
+}
+
+cpq_status cpq_commands_profiled_info(cpq_commands* cmds, size_t* recorded_ops, size_t* sample_capacity) {
+  if (!cmds) return fail(CPQ_ERR_INVALID_ARGUMENT, "profiled_info: NULL session");
+  if (recorded_ops) *recorded_ops = cmds->prof_ops.size();
+  if (sample_capacity) *sample_capacity = cmds->prof_events.size();
+  return CPQ_OK;
+}
+
+cpq_status cpq_commands_commit_wait_resolve(cpq_commands* cmds, cpq_gpu_segment* out, size_t cap,
+                                            size_t* n_out) {
+  if (!cmds || !n_out) return fail(CPQ_ERR_INVALID_ARGUMENT, "commit_wait_resolve: NULL argument");
+  *n_out = 0;
+  const size_t n = cmds->prof_ops.size();
+  if (n > cap || (n && !out))
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "commit_wait_resolve: room for " + std::to_string(cap) +
+                                              " segments, the batch recorded " + std::to_string(n));
+  cpq_status st = close_profiled_op(cmds);
+  if (st == CPQ_OK) st = cpq_commands_commit_and_wait(cmds);
+  std::vector<cpq_commands::ProfiledOp> ops;
+  ops.swap(cmds->prof_ops);  // a new batch starts whatever happens below
+  cmds->prof_cursor = 0;
+  cmds->prof_open = false;
+  if (st != CPQ_OK) return st;
+  cmds->prof_resolved_labels.clear();
+  for (const auto& op : ops) cmds->prof_resolved_labels.push_back(op.label);
+  // Offsets from the first op's start; each window from its own event pair,
+  // so a window's length keeps full precision however late in the batch.
+  for (size_t i = 0; i < n; ++i) {
+    float off_ms = 0.0f, len_ms = 0.0f;
+    hipError_t e = hipEventElapsedTime(&off_ms, cmds->prof_events[ops[0].start], cmds->prof_events[ops[i].start]);
+    if (e == hipSuccess) e = hipEventElapsedTime(&len_ms, cmds->prof_events[ops[i].start], cmds->prof_events[ops[i].end]);
+    if (e != hipSuccess) return hip_fail(e, "GpuSampler::resolve: hipEventElapsedTime");
+    const uint64_t s = (uint64_t)(std::max(0.0, (double)off_ms * 1e6) + 0.5);
+    const uint64_t d = (uint64_t)(std::max(0.0, (double)len_ms * 1e6) + 0.5);
+    out[i] = cpq_gpu_segment{cmds->prof_resolved_labels[i].c_str(), s, s + d};
+  }
+  *n_out = n;
+  return CPQ_OK;
+}
+
+cpq_status cpq_completion_result(int hip_error) {
+  const hipError_t e = static_cast<hipError_t>(hip_error);
+  if (e == hipSuccess) return CPQ_OK;
+  return fail(CPQ_ERR_COMMAND_BUFFER_FAILED, std::string("GPU command stream failed: ") + hipGetErrorName(e) +
+                                                 " (" + hipGetErrorString(e) + ")");
 }
 
 // ---------------------------------------------------------------------------

@@ -4,6 +4,7 @@ crate, crates/cider-press-kernels/src/lib.rs:35-40), backed by libcpq.so.
     Device.system_default()        -> device.rs:77
     device.alloc_buffer / upload   -> device.rs:167-233 (512-B rounding, zeroed slack)
     device.commands()              -> device.rs:319 (one in-order HIP stream)
+    device.commands_profiled(n)    -> device.rs:465-470 (per-op GPU windows, gpu_sampler.rs)
     Commands.commit / wait         -> commands.rs:349-419
     KernelLibrary.quantized(dev)   -> library.rs:230 (kernels are compiled ahead of time)
     kernels.{qmv,qmm,dequantize,gather,embed}.*  -> kernels/{qmv,qmm,dequantize}.rs, nn.rs
@@ -71,6 +72,22 @@ class Device:
         _lib.check(self._lib.cpq_commands_wrap_stream(self._h, ctypes.c_void_p(hip_stream), ctypes.byref(h)))
         return Commands(self, h)
 
+    def commands_profiled(self, op_capacity: int) -> "Commands":
+        """A session that times up to `op_capacity` ops per batch (commands.rs:465-470)."""
+        h = ctypes.c_void_p()
+        _lib.check(self._lib.cpq_commands_create_profiled(self._h, op_capacity, ctypes.byref(h)))
+        return Commands(self, h)
+
+    def supports_stage_boundary_sampling(self) -> bool:
+        """device.rs:314-322; always true on an in-order HIP stream."""
+        return bool(self._lib.cpq_device_supports_stage_boundary_sampling(self._h))
+
+    def gpu_timestamp_period_ns(self) -> float:
+        """Nanoseconds per GpuSegment tick (device.rs:324-368)."""
+        v = ctypes.c_double()
+        _lib.check(self._lib.cpq_device_gpu_timestamp_period_ns(self._h, ctypes.byref(v)))
+        return float(v.value)
+
     def __del__(self):
         if getattr(self, "_h", None) and self._lib is not None:
             self._lib.cpq_device_release(self._h)
@@ -130,6 +147,26 @@ class Buffer:
             self.ptr = None
 
 
+class _Segment(ctypes.Structure):
+    _fields_ = [("label", ctypes.c_char_p), ("start_tick", ctypes.c_uint64), ("end_tick", ctypes.c_uint64)]
+
+
+class GpuSegment:
+    """One timed op: label and GPU window in ticks (gpu_sampler.rs:22-42)."""
+
+    __slots__ = ("label", "start_tick", "end_tick")
+
+    def __init__(self, label: str, start_tick: int, end_tick: int):
+        self.label, self.start_tick, self.end_tick = label, start_tick, end_tick
+
+    def ticks(self) -> int:
+        """end - start, saturating at 0."""
+        return max(0, self.end_tick - self.start_tick)
+
+    def __repr__(self):
+        return f"GpuSegment({self.label!r}, {self.start_tick}, {self.end_tick})"
+
+
 class Commands:
     """A command session on one HIP stream (commands.rs)."""
 
@@ -155,6 +192,43 @@ class Commands:
 
     def commit_and_wait(self) -> None:
         _lib.check(self._lib.cpq_commands_commit_and_wait(self._h))
+
+    # Encoder hazard hooks (commands.rs:139-153, 290-296): an in-order stream
+    # already orders every launch, so these only validate the session.
+    def record_input(self, key: int) -> None:
+        _lib.check(self._lib.cpq_commands_record_input(self._h, key))
+
+    def record_output(self, key: int) -> None:
+        _lib.check(self._lib.cpq_commands_record_output(self._h, key))
+
+    def record_unresolved_input(self) -> None:
+        _lib.check(self._lib.cpq_commands_record_unresolved_input(self._h))
+
+    def elide_next_barrier(self) -> None:
+        _lib.check(self._lib.cpq_commands_elide_next_barrier(self._h))
+
+    def begin_profiled_op(self, label: str) -> None:
+        """End the open op's window and open one for `label` (commands.rs:163-181)."""
+        _lib.check(self._lib.cpq_commands_begin_profiled_op(self._h, label.encode()))
+
+    def recorded_ops(self) -> int:
+        n = ctypes.c_size_t()
+        _lib.check(self._lib.cpq_commands_profiled_info(self._h, ctypes.byref(n), None))
+        return n.value
+
+    def sample_capacity(self) -> int:
+        """Timestamp slots: two per op of capacity (gpu_sampler.rs:86-90)."""
+        n = ctypes.c_size_t()
+        _lib.check(self._lib.cpq_commands_profiled_info(self._h, None, ctypes.byref(n)))
+        return n.value
+
+    def commit_wait_resolve(self) -> list:
+        """Wait, then one GpuSegment per recorded op (commands.rs:361-374)."""
+        cap = self.recorded_ops()
+        arr = (_Segment * max(cap, 1))()
+        n = ctypes.c_size_t()
+        _lib.check(self._lib.cpq_commands_commit_wait_resolve(self._h, arr, cap, ctypes.byref(n)))
+        return [GpuSegment(arr[i].label.decode(), arr[i].start_tick, arr[i].end_tick) for i in range(n.value)]
 
     def begin_capture(self) -> None:
         """Record (not run) everything encoded until end_capture into a HIP graph."""

@@ -84,14 +84,23 @@ class QuantizedWeight:
     @staticmethod
     def from_bytes(device: Device, shape, quantization: Quantization, weights, scales, biases,
                    dtype: str = "bf16") -> "QuantizedWeight":
-        n, k = shape
+        n, k = QuantizedWeight._rank2(shape)
         return QuantizedWeight._make(device, n, k, k, quantization, weights, scales, biases, dtype)
 
     @staticmethod
     def from_bytes_k_padded(device: Device, shape, k_logical: int, quantization: Quantization, weights, scales,
                             biases, dtype: str = "bf16") -> "QuantizedWeight":
-        n, k = shape
+        n, k = QuantizedWeight._rank2(shape)
         return QuantizedWeight._make(device, n, k, k_logical, quantization, weights, scales, biases, dtype)
+
+    @staticmethod
+    def _rank2(shape):
+        """[N, K] or InvalidArgument (quantized.rs:137-143)."""
+        dims = tuple(int(d) for d in shape)
+        if len(dims) != 2:
+            raise _lib.InvalidArgument(f"QuantizedWeight: shape must be rank 2 ([N, K]); got rank {len(dims)} "
+                                       f"({list(dims)})")
+        return dims
 
     @staticmethod
     def _make(device, n, k_phys, k_log, q, weights, scales, biases, dtype):

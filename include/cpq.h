@@ -124,7 +124,75 @@ cpq_status cpq_commands_end_capture(cpq_commands* cmds, cpq_graph** out);
 cpq_status cpq_graph_launch(cpq_graph* graph, cpq_commands* cmds);
 void cpq_graph_release(cpq_graph* graph);
 
-/* GPU timing on a session's stream (replaces GpuSampler, gpu_sampler.rs). */
+/* Encoder hazard hooks of the reference's runtime (commands.rs:139-153
+ * record_output / record_input / record_unresolved_input, commands.rs:290-296
+ * elide_next_barrier), called by its graph evaluator around every op
+ * (eval.rs:280-292, 450-462).  They feed Metal's cross-encoder fences and
+ * per-dispatch buffer barriers.  A session here is one in-order HIP stream,
+ * so every launch already starts after the previous one has finished and
+ * there is no fence or barrier to add or elide: the hooks check the session
+ * and return CPQ_OK, and ops behave exactly as without them.  Eliding a
+ * barrier is only ever an allowed overlap in the reference, never required.
+ * (dispatch_threads / dispatch_threadgroups, commands.rs:298-330, have no
+ * counterpart: every op launches its own grid.) */
+cpq_status cpq_commands_record_input(cpq_commands* cmds, uint64_t key);
+cpq_status cpq_commands_record_output(cpq_commands* cmds, uint64_t key);
+cpq_status cpq_commands_record_unresolved_input(cpq_commands* cmds);
+cpq_status cpq_commands_elide_next_barrier(cpq_commands* cmds);
+
+/* Per-op GPU timing of a session (GpuSampler, gpu_sampler.rs:44-162, and the
+ * profiled-session calls of commands.rs:155-181, 361-374, 465-470). */
+
+/* One timed op: its label and its GPU execution window in ticks
+ * (GpuSegment, gpu_sampler.rs:22-42).  Ticks are nanoseconds on the GPU's
+ * timeline, counted from the start of the batch's first op. */
+typedef struct cpq_gpu_segment {
+  const char* label; /* valid until the next resolve or the session's release */
+  uint64_t start_tick;
+  uint64_t end_tick;
+} cpq_gpu_segment;
+
+/* Device::supports_stage_boundary_sampling (device.rs:314-322): 1.  A timing
+ * event can be recorded between any two launches of an in-order stream. */
+int cpq_device_supports_stage_boundary_sampling(cpq_device* dev);
+/* Device::gpu_timestamp_period_ns (device.rs:324-368): nanoseconds per tick
+ * of cpq_gpu_segment, 1.0 here. */
+cpq_status cpq_device_gpu_timestamp_period_ns(cpq_device* dev, double* out_ns_per_tick);
+/* Device::commands_profiled / Commands::new_profiled (commands.rs:155-161,
+ * 465-470): a session that can time up to op_capacity ops per batch (two
+ * timing events each, created here).  CPQ_ERR_HIP_API if op_capacity * 2
+ * overflows or the events cannot be created. */
+cpq_status cpq_commands_create_profiled(cpq_device* dev, size_t op_capacity, cpq_commands** out);
+/* Commands::begin_profiled_op (commands.rs:163-181): ends the open op's
+ * window (if any) and opens one for `label` (copied) covering everything
+ * encoded until the next begin_profiled_op or commit_wait_resolve.  No-op on
+ * an ordinary session.  Past op_capacity ops it stops timing further ops
+ * instead of failing (the resolved batch has fewer segments).  The GPU runs
+ * work as it is encoded, so an op's window also holds any time the GPU sat
+ * idle waiting for the host to encode it.  CPQ_ERR_INVALID_ARGUMENT while
+ * the stream is being captured into a graph. */
+cpq_status cpq_commands_begin_profiled_op(cpq_commands* cmds, const char* label);
+/* Ops recorded in the current batch, and the timestamp capacity (2 per op:
+ * GpuSampler::recorded_segments().len(), sample_capacity()). */
+cpq_status cpq_commands_profiled_info(cpq_commands* cmds, size_t* recorded_ops, size_t* sample_capacity);
+/* Commands::commit_wait_resolve (commands.rs:361-374) with
+ * GpuSampler::resolve (gpu_sampler.rs:121-162): ends the open op's window,
+ * waits for the session exactly as cpq_commands_wait (same statuses), then
+ * writes one segment per recorded op, in encode order, to out[0..*n_out)
+ * and starts a new batch.  cap must hold the recorded ops
+ * (CPQ_ERR_INVALID_ARGUMENT before waiting otherwise).  On an ordinary
+ * session: waits and returns 0 segments. */
+cpq_status cpq_commands_commit_wait_resolve(cpq_commands* cmds, cpq_gpu_segment* out, size_t cap,
+                                            size_t* n_out);
+
+/* Maps the HIP status of a finished stream to the status cpq_commands_wait
+ * returns (commands.rs:378-400 completion_result): CPQ_OK for hipSuccess,
+ * else CPQ_ERR_COMMAND_BUFFER_FAILED with the HIP error's name and text as
+ * the message.  Exported so the mapping can be checked without a failing
+ * GPU. */
+cpq_status cpq_completion_result(int hip_error);
+
+/* GPU timing on a session's stream between two recorded events. */
 cpq_status cpq_event_create(cpq_event** out);
 cpq_status cpq_event_record(cpq_event* ev, cpq_commands* cmds);
 cpq_status cpq_event_elapsed_ms(cpq_event* start, cpq_event* end, float* out_ms);

@@ -181,3 +181,37 @@ def test_null_session_is_invalid_argument():
     L = _lib.lib()
     st = L.cpq_affine_qmv(None, BF16, None, 0, None, 0, None, 0, None, 0, None, 0, 0, 64, 4)
     assert st == _lib.INVALID_ARGUMENT
+
+
+def test_completion_result_maps_stream_status():
+    """A finished stream's HIP status maps to the session status the way
+    completion_result does (commands.rs:378-400 and its unit tests at
+    commands.rs:481-500): success is OK, any failure is CommandBufferFailed
+    carrying the runtime's description."""
+    L = _lib.lib()
+    assert L.cpq_completion_result(0) == _lib.OK
+    for code, name in ((700, "hipErrorIllegalAddress"), (719, "hipErrorLaunchFailure")):
+        assert L.cpq_completion_result(code) == _lib.COMMAND_BUFFER_FAILED
+        msg = L.cpq_last_error_message().decode()
+        assert msg.startswith("GPU command stream failed: ") and name in msg, msg
+    with pytest.raises(_lib.CommandBufferFailed, match="hipErrorIllegalAddress"):
+        _lib.check(L.cpq_completion_result(700))
+
+
+def test_session_hooks_reject_null_session():
+    """The encoder hooks and profiled-session calls validate their session
+    before anything else (no GPU needed)."""
+    import ctypes
+
+    L = _lib.lib()
+    assert L.cpq_commands_record_input(None, 1) == _lib.INVALID_ARGUMENT
+    assert L.cpq_commands_record_output(None, 1) == _lib.INVALID_ARGUMENT
+    assert L.cpq_commands_record_unresolved_input(None) == _lib.INVALID_ARGUMENT
+    assert L.cpq_commands_elide_next_barrier(None) == _lib.INVALID_ARGUMENT
+    assert L.cpq_commands_begin_profiled_op(None, b"x") == _lib.INVALID_ARGUMENT
+    n = ctypes.c_size_t(7)
+    assert L.cpq_commands_commit_wait_resolve(None, None, 0, ctypes.byref(n)) == _lib.INVALID_ARGUMENT
+    assert L.cpq_commands_profiled_info(None, None, None) == _lib.INVALID_ARGUMENT
+    assert L.cpq_device_supports_stage_boundary_sampling(None) == 0
+    h = ctypes.c_void_p()
+    assert L.cpq_commands_create_profiled(None, 4, ctypes.byref(h)) == _lib.INVALID_ARGUMENT
