@@ -30,7 +30,7 @@ SOURCES = [
     "kernels/skinny.hip",
     "kernels/qmm.hip",
     "kernels/qmm_wide.hip",
-    "kernels/qmm_dma.hip",
+    "kernels/qmm_dma.hip", "kernels/qmm_small.hip",
     "kernels/qmm_n.hip",
     "kernels/gather.hip",
     "kernels/moe.hip",

@@ -113,6 +113,10 @@ hipError_t launch_embed(hipStream_t s, const QuantArgs& q, const uint32_t* ids, 
 
 // Decode GEMV: y[N] = x[K] . W^T for one activation row.
 hipError_t launch_qmv(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k);
+// The decode layout for up to 16 rows: Y[M, N] = X[M, K] . W^T (shape limits
+// in qmv_rows_fits).
+bool qmv_rows_fits(const QuantArgs& q, int m, int n, int k, const void* x);
+hipError_t launch_qmv_rows(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k);
 
 // Small-M GEMM on the matrix cores with VALU dequantization (M rows, any M;
 // processed 16 rows at a time).  Also the gather kernel body.
@@ -191,6 +195,22 @@ hipError_t launch_gather_qmm(hipStream_t s, const QuantArgs& q, const void* x, i
 // Whether the small-M kernel's per-slab constants fit in LDS at this K and
 // group size (16 columns x (K/gs + 1) x 16 bytes next to its static LDS).
 bool skinny_fits(int k, int gs);
+
+// Small-M kernel (kernels/qmm_small.hip), 1 <= M <= 64 at 4 and 8 bits, K a
+// multiple of 256: K parts per column tile, chunks per part, K elements per
+// chunk, 16-row blocks (the tile is 16*mb columns) and the split-K scratch it
+// needs.  split == 0: the shape is not supported (or its split would need
+// more scratch than scratch_cap).
+struct SmallPlan {
+  int split;
+  int nch;
+  int kb;
+  int mb;
+  size_t scratch_bytes;
+};
+SmallPlan qmm_small_plan(const QuantArgs& q, int m, int n, int k, int cu_count, size_t scratch_cap);
+hipError_t launch_qmm_small(hipStream_t s, const SmallPlan& p, void* scratch, const QuantArgs& q, const void* x,
+                            void* y, int m, int n, int k);
 
 // Row-count threshold below which cpq_quantized_matmul uses the skinny kernel.
 int skinny_max_m(const QuantArgs& q, int n, int k);

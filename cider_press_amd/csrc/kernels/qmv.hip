@@ -25,6 +25,9 @@
 //     as v_mfma_f32_16x16x32 against the activation slice broadcast to all 16
 //     A rows (the matrix cores are otherwise idle at M = 1);
 //   - the K-partial results of the waves are summed through LDS.
+#include <algorithm>
+#include <type_traits>
+
 #include "../cpq_internal.hpp"
 #include "common.hpp"
 
@@ -290,15 +293,17 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_kernel(const uint32_t* __restr
 constexpr int kLeanXItems = 8;   // 16-B activation items per lane (K <= 16384)
 constexpr int kLeanQuads = 8;    // 8-B scale/bias quads per lane (wave's groups per row <= 128)
 
-// Per-wave LDS: activations (256 B per step) then constants [16][GW + 1].
-__host__ __device__ constexpr size_t lean_wave_lds(int nsteps, int gs_shift) {
-  return (size_t)256 * nsteps + (size_t)16 * ((size_t)nsteps * (128 >> gs_shift) + 1) * 16;
+// Per-wave LDS: activations (256 B per step and row) then constants [16][GW + 1].
+__host__ __device__ constexpr size_t lean_wave_lds(int nsteps, int gs_shift, int rows = 1) {
+  return (size_t)256 * nsteps * rows + (size_t)16 * ((size_t)nsteps * (128 >> gs_shift) + 1) * 16;
 }
 
-template <typename TT, int BITS, int GS_SHIFT, int PF, bool ONE, bool FAST>
+// MR > 1: xbase holds the lane's slice-0 address; slice i of step j sits at
+// xbase + xsw[i] + j * STEP_X (per-lane swizzled offsets of its row).
+template <typename TT, int BITS, int GS_SHIFT, int PF, bool ONE, bool FAST, int MR = 1>
 __device__ __forceinline__ f32x4 lean_stream(__amdgpu_buffer_rsrc_t wr, uint32_t voff, int nsteps,
                                              const unsigned char* cbase, const unsigned char* xbase,
-                                             uint32_t (&buf)[PF][BITS]) {
+                                             uint32_t (&buf)[PF][BITS], const int* xsw = nullptr) {
   constexpr int CB = BITS * 4;             // bytes per 32-element chunk
   constexpr int STEP_W = 4 * CB;           // weight bytes a lane group advances per step
   constexpr int STEP_C = (128 >> GS_SHIFT) * 16;  // constants bytes per step
@@ -306,13 +311,25 @@ __device__ __forceinline__ f32x4 lean_stream(__amdgpu_buffer_rsrc_t wr, uint32_t
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   auto step = [&](const uint32_t* cur, int j) {
     const f32x4 gc = *reinterpret_cast<const f32x4*>(cbase + j * STEP_C);
-    const u32x4* xa = reinterpret_cast<const u32x4*>(xbase + j * STEP_X);
     const float sc = gc[0], b = gc[1], c0 = gc[2], c1 = gc[3];
     const float s16 = sc * 0.0625f;
-    acc = Mfma16<TT>::run(xa[0], dequant_slice<TT, BITS, FAST, 0>(cur, sc, s16, b, c0, c1), acc);
-    acc = Mfma16<TT>::run(xa[1], dequant_slice<TT, BITS, FAST, 1>(cur, sc, s16, b, c0, c1), acc);
-    acc = Mfma16<TT>::run(xa[2], dequant_slice<TT, BITS, FAST, 2>(cur, sc, s16, b, c0, c1), acc);
-    acc = Mfma16<TT>::run(xa[3], dequant_slice<TT, BITS, FAST, 3>(cur, sc, s16, b, c0, c1), acc);
+    if constexpr (MR == 1) {
+      const u32x4* xa = reinterpret_cast<const u32x4*>(xbase + j * STEP_X);
+      acc = Mfma16<TT>::run(xa[0], dequant_slice<TT, BITS, FAST, 0>(cur, sc, s16, b, c0, c1), acc);
+      acc = Mfma16<TT>::run(xa[1], dequant_slice<TT, BITS, FAST, 1>(cur, sc, s16, b, c0, c1), acc);
+      acc = Mfma16<TT>::run(xa[2], dequant_slice<TT, BITS, FAST, 2>(cur, sc, s16, b, c0, c1), acc);
+      acc = Mfma16<TT>::run(xa[3], dequant_slice<TT, BITS, FAST, 3>(cur, sc, s16, b, c0, c1), acc);
+    } else {
+      const unsigned char* xj = xbase + j * STEP_X;
+      const u32x4 a0 = *reinterpret_cast<const u32x4*>(xj + xsw[0]);
+      const u32x4 a1 = *reinterpret_cast<const u32x4*>(xj + xsw[1]);
+      const u32x4 a2 = *reinterpret_cast<const u32x4*>(xj + xsw[2]);
+      const u32x4 a3 = *reinterpret_cast<const u32x4*>(xj + xsw[3]);
+      acc = Mfma16<TT>::run(a0, dequant_slice<TT, BITS, FAST, 0>(cur, sc, s16, b, c0, c1), acc);
+      acc = Mfma16<TT>::run(a1, dequant_slice<TT, BITS, FAST, 1>(cur, sc, s16, b, c0, c1), acc);
+      acc = Mfma16<TT>::run(a2, dequant_slice<TT, BITS, FAST, 2>(cur, sc, s16, b, c0, c1), acc);
+      acc = Mfma16<TT>::run(a3, dequant_slice<TT, BITS, FAST, 3>(cur, sc, s16, b, c0, c1), acc);
+    }
   };
   int base = 0;
   // ONE: the whole range is the PF prefetched steps (no loop, buffers consumed in place).
@@ -450,6 +467,151 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_lean_kernel(const uint32_t* __
   }
 }
 
+// Up to 16 activation rows on the lean kernel's layout: the same workgroup
+// (16 output columns, WAVES waves over K, each wave self-contained until the
+// final sum), but each wave stages M rows of its activation range, row r at
+// r * 256 * nsteps bytes of its region with 16-byte slot s of a step stored
+// at slot s ^ r, so the 16 A rows of one MFMA read 16 distinct slots.  Rows
+// past M are not read: their A rows only feed output rows that are never
+// stored.  NST steps per wave (K = 128 * WAVES * NST); at most 16
+// activation items per lane (M * NST <= 64).
+template <typename TT, int BITS, int GS_SHIFT, int WAVES, int NST>
+__global__ __launch_bounds__(64 * WAVES) void qmm_lean_rows_kernel(const uint32_t* __restrict__ w,
+                                                                    const uint16_t* __restrict__ scales,
+                                                                    const uint16_t* __restrict__ biases,
+                                                                    const uint16_t* __restrict__ x,
+                                                                    uint16_t* __restrict__ y, int m, int n, int k) {
+  constexpr int CB = BITS * 4;
+  constexpr int GPS = 128 >> GS_SHIFT;
+  constexpr int XMAX = 16;             // activation items per lane
+  constexpr int IPR = NST / 4;         // items per row and lane
+  constexpr int PF = NST < 8 ? NST : 8;
+  constexpr bool ONE = NST == PF;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int G = k >> GS_SHIFT;
+  constexpr int nsteps = NST;
+  const int GW = nsteps * GPS;
+  const int quads = GW >> 2;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int u0 = wave * nsteps;
+  const int rows = min(m, 16);
+  const int RB = 256 * nsteps;  // bytes of one activation row in a wave's region
+  const uint32_t rowbytes = (uint32_t)k * BITS / 8;
+  const size_t wlds = lean_wave_lds(nsteps, GS_SHIFT, rows);
+  unsigned char* xw = smem + (size_t)wave * wlds;
+  f32x4* cw = reinterpret_cast<f32x4*>(xw + (size_t)RB * rows);  // [16][GW + 1]
+  f32x4* red = reinterpret_cast<f32x4*>(smem + (size_t)WAVES * wlds);  // [WAVES][64]
+
+  const __amdgpu_buffer_rsrc_t wr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)w, 0, (int)((uint32_t)n * rowbytes), 0x00020000);
+  const __amdgpu_buffer_rsrc_t sr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)scales, 0, (int)((uint32_t)n * (uint32_t)G * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t br =
+      __builtin_amdgcn_make_buffer_rsrc((void*)biases, 0, (int)((uint32_t)n * (uint32_t)G * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)x, 0, (int)((uint32_t)m * (uint32_t)k * 2u), 0x00020000);
+
+  // 1. Small loads first: this wave's scale / bias quads, then its
+  //    activation items (row rr, item t: bytes 1024 t + 16 lane of the row's
+  //    range).
+  const int cr = lane >> 2;
+  const uint32_t coff = ((uint32_t)(n0 + cr) * (uint32_t)G + (uint32_t)(u0 * GPS + 4 * (lane & 3))) * 2u;
+  u32x2 sv[kLeanQuads], bv[kLeanQuads];
+#pragma unroll
+  for (int t = 0; t < kLeanQuads; ++t) {
+    sv[t] = bv[t] = u32x2{0u, 0u};
+    if (4 * t < quads) {
+      sv[t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(sr, coff + 32u * t, 0, 0));
+      bv[t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(br, coff + 32u * t, 0, 0));
+    }
+  }
+  const uint32_t xoff = (uint32_t)u0 * 256u + (uint32_t)lane * 16u;
+  u32x4 xv[XMAX];
+#pragma unroll
+  for (int i = 0; i < XMAX; ++i) {
+    const int rr = i / IPR, t = i % IPR;
+    if (rr < rows)
+      xv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            xr, xoff + 1024u * t, (int)((uint32_t)rr * (uint32_t)k * 2u), 0));
+  }
+
+  // 2. The weight stream.
+  const uint32_t voff = (uint32_t)(n0 + r) * rowbytes + (uint32_t)(4 * u0 + g) * CB;
+  uint32_t buf[PF][BITS];
+#pragma unroll
+  for (int p = 0; p < PF; ++p) lean_load<BITS>(wr, voff + p * 4 * CB, 0, buf[p]);
+
+  // 3. Stage this wave's activations and constants, vote within the wave.
+#pragma unroll
+  for (int i = 0; i < XMAX; ++i) {
+    const int rr = i / IPR, t = i % IPR;
+    if (rr < rows)
+      *reinterpret_cast<u32x4*>(xw + rr * RB + 1024 * t + (lane >> 4) * 256 + (((lane & 15) ^ rr) << 4)) =
+          interleave_x<BITS>(xv[i]);
+  }
+  FastQuick fq;
+  fast_quick_init(fq);
+  const int cwp = GW + 1;
+#pragma unroll
+  for (int t = 0; t < kLeanQuads; ++t) {
+    const int cq = (lane & 3) + 4 * t;
+    if (4 * t < quads && cq < quads) {
+      f32x4* dst = cw + cr * cwp + cq * 4;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        dst[2 * h] = group_consts<TT>(sv[t][h] & 0xffffu, bv[t][h] & 0xffffu);
+        dst[2 * h + 1] = group_consts<TT>(sv[t][h] >> 16, bv[t][h] >> 16);
+        fast_quick_add<TT>(fq, sv[t][h], bv[t][h]);
+      }
+    }
+  }
+  bool ok = true;
+  if (!fast_quick_ok<TT>(fq)) {
+#pragma unroll
+    for (int t = 0; t < kLeanQuads; ++t) {
+      const int cq = (lane & 3) + 4 * t;
+      if (4 * t < quads && cq < quads) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          ok &= fast_ok_bits<TT>(sv[t][h] & 0xffffu, bv[t][h] & 0xffffu) &
+                fast_ok_bits<TT>(sv[t][h] >> 16, bv[t][h] >> 16);
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const bool fast = __builtin_amdgcn_ballot_w64(!ok) == 0;
+
+  // 4. Stream: lane (row r, group g) reads slice i of step j at
+  //    xw + r * RB + j * 256 + ((4g + i) ^ r) * 16.
+  const unsigned char* cbase = reinterpret_cast<const unsigned char*>(cw + r * cwp + ((g * 32) >> GS_SHIFT));
+  const unsigned char* xbase = xw + r * RB;
+  int xsw[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xsw[i] = ((4 * g + i) ^ r) << 4;
+  const f32x4 acc = fast ? lean_stream<TT, BITS, GS_SHIFT, PF, ONE, true, 16>(wr, voff, nsteps, cbase, xbase, buf, xsw)
+                         : lean_stream<TT, BITS, GS_SHIFT, PF, ONE, false, 16>(wr, voff, nsteps, cbase, xbase, buf, xsw);
+
+  // 5. The waves' K ranges in order; element i of lane (r, g) is output row
+  //    4g + i, column n0 + r.
+  red[wave * 64 + lane] = acc;
+  __syncthreads();
+  if (wave == 0 && n0 + r < n) {
+    f32x4 v = red[lane];
+#pragma unroll
+    for (int i = 1; i < WAVES; ++i) v = v + red[i * 64 + lane];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * g + i;
+      if (row < m) y[(size_t)row * n + n0 + r] = TT::from_f32(v[i]);
+    }
+  }
+}
+
 int shift_of(int gs) {
   int s = 0;
   while ((1 << s) < gs) ++s;
@@ -544,6 +706,40 @@ bool lean_fits(const QuantArgs& q, int n, int k, int waves) {
   return ((reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases)) & 7u) == 0;
 }
 
+template <typename TT, int BITS, int GS_SHIFT, int NST>
+hipError_t launch_rows_cfg(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
+                           size_t lds) {
+  if (lds > 64 * 1024) {
+    static const hipError_t attr = [] {
+      const void* fn = reinterpret_cast<const void*>(&qmm_lean_rows_kernel<TT, BITS, GS_SHIFT, 8, NST>);
+      hipFuncAttributes fa;
+      hipError_t e = hipFuncGetAttributes(&fa, fn);
+      if (e != hipSuccess) return e;
+      return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)(160 * 1024 - fa.sharedSizeBytes));
+    }();
+    if (attr != hipSuccess) return attr;
+  }
+  hipLaunchKernelGGL((qmm_lean_rows_kernel<TT, BITS, GS_SHIFT, 8, NST>), dim3((unsigned)((n + 15) / 16)), dim3(512),
+                     lds, s, q.w, static_cast<const uint16_t*>(q.scales), static_cast<const uint16_t*>(q.biases),
+                     static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), m, n, k);
+  return hipGetLastError();
+}
+
+template <typename TT, int BITS, int GS_SHIFT>
+hipError_t launch_rows_gs(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
+                          size_t lds) {
+  const int nst = k / 1024;
+  if (nst == 4) return launch_rows_cfg<TT, BITS, GS_SHIFT, 4>(s, q, x, y, m, n, k, lds);
+  if (nst == 8) return launch_rows_cfg<TT, BITS, GS_SHIFT, 8>(s, q, x, y, m, n, k, lds);
+  return launch_rows_cfg<TT, BITS, GS_SHIFT, 16>(s, q, x, y, m, n, k, lds);
+}
+
+size_t rows_lds(int m, int k, int gs) {
+  const int nst = k / 1024;
+  return (size_t)8 * lean_wave_lds(nst, shift_of(gs), std::min(m, 16)) + (size_t)8 * 64 * 16;
+}
+
 template <typename TT, int BITS>
 hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k) {
   const size_t G = (size_t)k / q.gs;
@@ -600,6 +796,39 @@ hipError_t launch_bits(hipStream_t s, const QuantArgs& q, const void* x, void* y
 }
 
 }  // namespace
+
+// Up to 16 rows on the lean layout: 4/8-bit, gs 32/64/128, K in
+// {4096, 8192, 16384} (8 waves of 4, 8 or 16 steps), M * K / 1024 <= 64
+// activation items per lane, LDS within the CU, 32-bit buffer ranges,
+// 8-byte aligned scales and biases, 16-byte aligned x.
+bool qmv_rows_fits(const QuantArgs& q, int m, int n, int k, const void* x) {
+  if ((q.bits != 4 && q.bits != 8) || (q.dtype != CPQ_DTYPE_BF16 && q.dtype != CPQ_DTYPE_F16)) return false;
+  if (q.gs != 32 && q.gs != 64 && q.gs != 128) return false;
+  if (m < 1 || m > 16 || n < 1 || (k != 4096 && k != 8192 && k != 16384)) return false;
+  if (m * (k / 1024) > 64) return false;
+  if (rows_lds(m, k, q.gs) > 160 * 1024 - 1024) return false;
+  if ((uint64_t)n * (uint64_t)k * q.bits / 8 >= (1ull << 31)) return false;
+  if ((uint64_t)n * (uint64_t)(k / q.gs) * 2 >= (1ull << 31)) return false;
+  if ((uint64_t)m * (uint64_t)k * 2 >= (1ull << 31)) return false;
+  return ((reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases)) & 7u) == 0 &&
+         (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+}
+
+hipError_t launch_qmv_rows(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k) {
+  const size_t lds = rows_lds(m, k, q.gs);
+  auto by_gs = [&](auto tt, auto bits) -> hipError_t {
+    using TT = decltype(tt);
+    constexpr int B = decltype(bits)::value;
+    if (q.gs == 32) return launch_rows_gs<TT, B, 5>(s, q, x, y, m, n, k, lds);
+    if (q.gs == 64) return launch_rows_gs<TT, B, 6>(s, q, x, y, m, n, k, lds);
+    return launch_rows_gs<TT, B, 7>(s, q, x, y, m, n, k, lds);
+  };
+  using B4 = std::integral_constant<int, 4>;
+  using B8 = std::integral_constant<int, 8>;
+  if (q.dtype == CPQ_DTYPE_BF16) return q.bits == 4 ? by_gs(BF16{}, B4{}) : by_gs(BF16{}, B8{});
+  if (q.dtype == CPQ_DTYPE_F16) return q.bits == 4 ? by_gs(F16{}, B4{}) : by_gs(F16{}, B8{});
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_qmv(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k) {
   if (q.dtype == CPQ_DTYPE_BF16) return launch_bits<BF16>(s, q, x, y, n, k);

@@ -23,14 +23,14 @@ bool kernel_available(cpq_dtype dtype, uint32_t group_size, uint32_t bits) {
   return t_ok && gs_ok && b_ok;
 }
 
-// Largest M the routed op sends to the small-M kernel (one 16-column slab of W
-// per workgroup, up to 64 activation rows per pass).  Up to 32 rows it always
-// wins; at 33..64 rows it wins while the prefill kernel's 128-wide tiles leave
-// most CUs idle (N <= 8192: measured 19.7 vs 26.5 us at M = 64, N = K = 4096)
-// and loses once N fills the chip (58 vs 31 us at N = 12288).
-// CPQ_SKINNY_MAX_M overrides it, read once per process.  Shapes whose slab
-// constants do not fit in LDS (K / gs beyond about 500 groups per row) never
-// take it.
+// Largest M the routed op sends to the small-M kernels (the decode layout for
+// up to 16 rows, the tiled small-M kernel, or the slab kernel; see
+// cpq_quantized_matmul).  Up to 32 rows they always win; at 33..64 rows they
+// win while the prefill kernel's 128-wide tiles leave most CUs idle (N <=
+// 8192) and lose once N fills the chip (slab kernel 58 vs 31 us at N =
+// 12288).  CPQ_SKINNY_MAX_M overrides it, read once per process.  Shapes
+// whose slab constants do not fit in LDS (K / gs beyond about 500 groups per
+// row) never take them.
 int skinny_max_m(const QuantArgs& q, int n, int k) {
   if (!skinny_fits(k, (int)q.gs)) return 0;  // its slab constants would not fit in LDS
   static const int lim = [] {
@@ -722,9 +722,35 @@ cpq_status cpq_quantized_matmul(cpq_commands* cmds, cpq_dtype dtype, const uint3
   st = cpq::check_ptrs("quantized_matmul", w_q, scales, biases, x, y);
   if (st != CPQ_OK) return st;
   cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
-  if ((long)m <= cpq::skinny_max_m(q, (int)n, (int)k_physical))
+  if ((long)m <= cpq::skinny_max_m(q, (int)n, (int)k_physical)) {
+    // Up to 16 rows at K = 4096 / 8192 / 16384 (4/8-bit): the decode kernel's
+    // layout with M activation rows.  Other 4/8-bit shapes with K a multiple
+    // of 256: the tiled small-M kernel.  Everything else: the slab kernel.
+    // CPQ_SMALL_M=0 forces the slab kernel, CPQ_QMV_ROWS=0 skips the decode
+    // layout (tuning hooks, read once per process).
+    static const bool small_on = [] {
+      const char* e = std::getenv("CPQ_SMALL_M");
+      return !(e && *e == '0');
+    }();
+    const bool words4 = ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(biases)) & 3u) == 0;
+    const cpq::SmallPlan sp = small_on && cpq::aligned16(x) && cpq::aligned16(w_q) && words4
+                                  ? cpq::qmm_small_plan(q, (int)m, (int)n, (int)k_physical, cmds->dev->cu_count,
+                                                        cmds->scratch ? cmds->scratch_bytes : 0)
+                                  : cpq::SmallPlan{0, 0, 0, 0, 0};
+    static const bool rows_on = [] {
+      const char* e = std::getenv("CPQ_QMV_ROWS");
+      return !(e && *e == '0');
+    }();
+    if (small_on && rows_on && cpq::qmv_rows_fits(q, (int)m, (int)n, (int)k_physical, x))
+      return cpq::launched(cpq::launch_qmv_rows(cmds->stream, q, x, y, (int)m, (int)n, (int)k_physical),
+                           "quantized_matmul (small-M) launch");
+    if (sp.split > 0)
+      return cpq::launched(
+          cpq::launch_qmm_small(cmds->stream, sp, cmds->scratch, q, x, y, (int)m, (int)n, (int)k_physical),
+          "quantized_matmul (small-M) launch");
     return cpq::launched(cpq::launch_qmm_skinny(cmds->stream, q, x, y, (int)m, (int)n, (int)k_physical),
                          "quantized_matmul (small-M) launch");
+  }
   return cpq::launched(cpq::launch_session_qmm(cmds, q, x, y, (int)m, (int)n, (int)k_physical),
                        "quantized_matmul (prefill) launch");
 }

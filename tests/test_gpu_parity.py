@@ -242,8 +242,9 @@ def test_quantized_matmul_routes_all_m(device, library, oracle, m, bits, gs):
     assert_tol(oracle, y, ref, x, k, "bf16", f"routed m={m}")
 
 
-# The small-M kernel runs 8 waves per workgroup when there are few 16-column
-# slabs and 4 otherwise, and takes up to 64 rows while N <= 8192.
+# Routed small-M shapes (up to 64 rows while N <= 8192) across the three
+# small-M kernels: the decode layout with M rows, the tiled small-M kernel and
+# the slab kernel.
 @pytest.mark.parametrize("m,n,k,bits,gs", [
     (5, 8192, 1024, 4, 64),     # 1 row block, 4 waves (512 slabs)
     (20, 8192, 1024, 8, 64),    # 2 row blocks, 4 waves
