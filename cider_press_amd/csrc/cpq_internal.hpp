@@ -96,6 +96,12 @@ int qmm_n_split(int m, int n, int k, int cu_count);
 size_t qmm_n_scratch_bytes(int m, int n, int split);
 hipError_t launch_qmm_n(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k, int split,
                         float* partial);
+// Decode (M = 1) transpose=false at 4/8 bits on the VALU; parts > 1 splits K
+// into fp32 partials (parts * N floats) added in order by a second kernel.
+bool qvm_fits(const QuantArgs& q, int n, int k);
+int qvm_parts(int n, int k, int cu_count);
+hipError_t launch_qvm(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k, int parts,
+                      float* partial);
 // Routed-expert plumbing (kernels/moe.hip): top-k routing, stable sort of
 // (token, slot) rows by expert, weighted combine back to tokens.
 size_t moe_sort_scratch_bytes(int rows, int n_experts);

@@ -148,6 +148,129 @@ __global__ __launch_bounds__(256) void qmm_n_reduce_kernel(const float* __restri
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode (M = 1) at 4 and 8 bits: y[n] = sum_k x[k] * RNE_T(fmaf(s, q, b))
+// on the VALU.  A workgroup (256 threads) owns 256 columns and one part of
+// K: thread (chunk c = tid % 8, row slot r = tid / 8) walks rows
+// k = k_lo + r, k_lo + r + 32, ... of the part, two rows at a time; per row
+// it reads the 32-column chunk c (one 16-byte load at 4-bit, the 8 threads of
+// a row slot reading 128 contiguous bytes) and its (scale, bias) word.  The
+// two rows' dequantized pairs (along n) are regrouped into pairs along k and
+// accumulated with one v_dot2 per two weights (products of two T exact in
+// fp32).  The (scale, bias) of row k is element k * G + group of the flat
+// tables; it is read as the aligned 4-byte word holding it (G may be odd).  The 32 row slots are then added through LDS in slot order; with
+// K split over parts, each part stores fp32 partial sums that
+// qmm_n_reduce_kernel adds in part order.  Rows past K, or past the part,
+// take x = 0 and zero constants (exact zeros).
+// ---------------------------------------------------------------------------
+constexpr int QV_COLS = 256, QV_SLOTS = 32;
+
+template <typename TT, int BITS>
+__global__ __launch_bounds__(256) void qvm_kernel(const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
+                                                  const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x,
+                                                  uint16_t* __restrict__ y, int n, int k, int gs_shift, int k_part,
+                                                  float* __restrict__ partial) {
+  __shared__ float red[QV_SLOTS][QV_COLS + 4];
+  const int tid = threadIdx.x;
+  const int c = tid & 7, rs = tid >> 3;
+  const int n0 = blockIdx.x * QV_COLS;
+  const int chunk = min((n0 >> 5) + c, (n >> 5) - 1);  // columns past N re-read the last chunk (not stored)
+  const int G = n >> gs_shift;
+  const int grp = (chunk << 5) >> gs_shift;
+  const uint32_t row_words = (uint32_t)n * BITS / 32;
+  const int k_lo = blockIdx.y * k_part, k_hi = min(k, k_lo + k_part);
+  const __amdgpu_buffer_rsrc_t wr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)w, 0, (int)((uint32_t)k * row_words * 4u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t sr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)scales, 0, (int)((uint32_t)k * (uint32_t)G * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t br =
+      __builtin_amdgcn_make_buffer_rsrc((void*)biases, 0, (int)((uint32_t)k * (uint32_t)G * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)x, 0, (int)((uint32_t)k * 2u), 0x00020000);
+  const uint32_t woff = (uint32_t)chunk * BITS * 4u;
+
+  float acc[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) acc[i] = 0.f;
+  // Two rows per step: ka = k_lo + rs + 64 j, kb = ka + 32.
+  for (int ka = k_lo + rs; ka < k_hi; ka += 2 * QV_SLOTS) {
+    const int kb = ka + QV_SLOTS;
+    const bool lb = kb < k_hi;
+    const int kbc = lb ? kb : ka;  // a row past the part re-reads row ka (zeroed below)
+    // Row offsets differ per row slot: they go into the per-lane offset.
+    const uint32_t wra = woff + (uint32_t)ka * row_words * 4u, wrb = woff + (uint32_t)kbc * row_words * 4u;
+    uint32_t wa[BITS], wb[BITS];
+#pragma unroll
+    for (int q = 0; q < BITS / 4; ++q) {
+      const u32x4 va = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, wra + 16u * q, 0, 0));
+      const u32x4 vb = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, wrb + 16u * q, 0, 0));
+      wa[4 * q] = va.x; wa[4 * q + 1] = va.y; wa[4 * q + 2] = va.z; wa[4 * q + 3] = va.w;
+      wb[4 * q] = vb.x; wb[4 * q + 1] = vb.y; wb[4 * q + 2] = vb.z; wb[4 * q + 3] = vb.w;
+    }
+    const uint32_t ea = (uint32_t)ka * (uint32_t)G + (uint32_t)grp, eb = (uint32_t)kbc * (uint32_t)G + (uint32_t)grp;
+    const uint32_t swa = __builtin_amdgcn_raw_buffer_load_b32(sr, (ea & ~1u) * 2u, 0, 0);
+    const uint32_t bwa = __builtin_amdgcn_raw_buffer_load_b32(br, (ea & ~1u) * 2u, 0, 0);
+    const uint32_t swb = __builtin_amdgcn_raw_buffer_load_b32(sr, (eb & ~1u) * 2u, 0, 0);
+    const uint32_t bwb = __builtin_amdgcn_raw_buffer_load_b32(br, (eb & ~1u) * 2u, 0, 0);
+    const bool ha = (ea & 1u) != 0, hb = (eb & 1u) != 0;
+    const uint32_t xwa = __builtin_amdgcn_raw_buffer_load_b32(xr, (uint32_t)(ka & ~1) * 2u, 0, 0);
+    const uint32_t xwb = __builtin_amdgcn_raw_buffer_load_b32(xr, (uint32_t)(kbc & ~1) * 2u, 0, 0);
+    const float sa = TT::to_f32((uint16_t)(ha ? swa >> 16 : swa & 0xffffu));
+    const float ba = TT::to_f32((uint16_t)(ha ? bwa >> 16 : bwa & 0xffffu));
+    const float sb = lb ? TT::to_f32((uint16_t)(hb ? swb >> 16 : swb & 0xffffu)) : 0.f;
+    const float bb = lb ? TT::to_f32((uint16_t)(hb ? bwb >> 16 : bwb & 0xffffu)) : 0.f;
+    const uint32_t xa = (ka & 1) ? xwa >> 16 : xwa & 0xffffu;
+    const uint32_t xb = lb ? ((kb & 1) ? xwb >> 16 : xwb & 0xffffu) : 0u;
+    const uint32_t xab = xa | (xb << 16);  // (x[ka], x[kb]) as a T pair
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {  // 8 columns 8p .. 8p+7 of the chunk
+      uint32_t ua[4], ub[4];
+      dequant8<TT, BITS, 0>(BITS == 4 ? &wa[p] : &wa[2 * p], sa, sa * 0.0625f, ba, ua);
+      dequant8<TT, BITS, 0>(BITS == 4 ? &wb[p] : &wb[2 * p], sb, sb * 0.0625f, bb, ub);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {  // ua[i] = (w[ka][n], w[ka][n+1]), n = 8p + 2i
+        const uint32_t lo = __builtin_amdgcn_perm(ub[i], ua[i], 0x05040100u);  // (w[ka][n], w[kb][n])
+        const uint32_t hi = __builtin_amdgcn_perm(ub[i], ua[i], 0x07060302u);  // (w[ka][n+1], w[kb][n+1])
+        acc[8 * p + 2 * i] = TT::dot2(lo, xab, acc[8 * p + 2 * i]);
+        acc[8 * p + 2 * i + 1] = TT::dot2(hi, xab, acc[8 * p + 2 * i + 1]);
+      }
+    }
+  }
+
+  // Row slots in order, then one part's sum per column.
+#pragma unroll
+  for (int i = 0; i < 32; ++i) red[rs][32 * c + i] = acc[i];
+  __syncthreads();
+  const int col = n0 + tid;
+  if (col < n) {
+    float v = red[0][tid];
+#pragma unroll
+    for (int r = 1; r < QV_SLOTS; ++r) v += red[r][tid];
+    if (partial)
+      partial[(size_t)blockIdx.y * n + col] = v;
+    else
+      y[col] = TT::from_f32(v);
+  }
+}
+
+template <typename TT, int BITS>
+hipError_t launch_qvm_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k, int parts,
+                        float* partial) {
+  int gs_shift = 0;
+  while ((1 << gs_shift) < q.gs) ++gs_shift;
+  const int k_part = (k + parts - 1) / parts;
+  const int np = (k + k_part - 1) / k_part;
+  const dim3 grid((unsigned)((n + QV_COLS - 1) / QV_COLS), (unsigned)np);
+  hipLaunchKernelGGL((qvm_kernel<TT, BITS>), grid, dim3(256), 0, s, q.w, static_cast<const uint16_t*>(q.scales),
+                     static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x),
+                     static_cast<uint16_t*>(y), n, k, gs_shift, k_part, np > 1 ? partial : nullptr);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || np <= 1) return e;
+  size_t blocks = ((size_t)n + 255) / 256;
+  hipLaunchKernelGGL((qmm_n_reduce_kernel<TT>), dim3((unsigned)blocks), dim3(256), 0, s, partial, np, (size_t)n,
+                     static_cast<uint16_t*>(y));
+  return hipGetLastError();
+}
+
 template <typename TT, int BITS>
 hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k, int split,
                     float* partial) {
@@ -197,6 +320,38 @@ int qmm_n_split(int m, int n, int k, int cu_count) {
 }
 
 size_t qmm_n_scratch_bytes(int m, int n, int split) { return split > 1 ? (size_t)split * m * n * 4 : 0; }
+
+// The decode kernel's K parts: about two workgroups per CU, each part at
+// least 256 rows (so the fixed per-workgroup work stays small next to it).
+int qvm_parts(int n, int k, int cu_count) {
+  const long blocks = (n + QV_COLS - 1) / QV_COLS;
+  const long want = 2L * (cu_count > 0 ? cu_count : 256);
+  int parts = 1;
+  while (blocks * parts * 2 <= want && k / (parts * 2) >= 256) parts *= 2;
+  return parts;
+}
+
+bool qvm_fits(const QuantArgs& q, int n, int k) {
+  if (q.bits != 4 && q.bits != 8) return false;
+  if (n % 32 != 0 || k < 1) return false;
+  if ((uint64_t)k * (uint64_t)n * q.bits / 8 >= (1ull << 31)) return false;
+  if ((uint64_t)k * (uint64_t)(n / q.gs) * 2 >= (1ull << 31)) return false;
+  // 16-byte weight loads, 4-byte scale/bias and x words.
+  return (reinterpret_cast<uintptr_t>(q.w) & 15u) == 0 &&
+         ((reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases)) & 3u) == 0;
+}
+
+hipError_t launch_qvm(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k, int parts,
+                      float* partial) {
+  if (parts > 1 && !partial) return hipErrorInvalidValue;
+  if (q.dtype == CPQ_DTYPE_BF16)
+    return q.bits == 4 ? launch_qvm_t<BF16, 4>(s, q, x, y, n, k, parts, partial)
+                       : launch_qvm_t<BF16, 8>(s, q, x, y, n, k, parts, partial);
+  if (q.dtype == CPQ_DTYPE_F16)
+    return q.bits == 4 ? launch_qvm_t<F16, 4>(s, q, x, y, n, k, parts, partial)
+                       : launch_qvm_t<F16, 8>(s, q, x, y, n, k, parts, partial);
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_qmm_n(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k, int split,
                         float* partial) {

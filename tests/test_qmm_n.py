@@ -31,8 +31,13 @@ def test_qmm_n_args():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("m,n,k,gs,bits,dtype", [
-    (1, 4096, 4096, 64, 4, "bf16"),     # qvm at the decode shape
-    (1, 1024, 1000, 32, 8, "f16"),      # qvm, ragged K tile
+    (1, 4096, 4096, 64, 4, "bf16"),     # qvm at the decode shape (VALU decode kernel, K in parts)
+    (1, 1024, 1000, 32, 8, "f16"),      # qvm, K not a multiple of the two-row step
+    (1, 12288, 4096, 64, 4, "bf16"),    # qvm, wide N
+    (1, 4128, 4096, 32, 4, "f16"),      # qvm, last column block partly past N; 129 groups a row
+    (1, 2048, 96, 32, 8, "bf16"),       # qvm, one part
+    (1, 96, 8192, 32, 4, "bf16"),       # qvm, one column block, many parts; 3 groups a row
+    (1, 1024, 2048, 32, 3, "bf16"),     # qvm at 3 bits: the tiled kernel
     (5, 256, 512, 64, 4, "bf16"),
     (130, 352, 264, 32, 4, "bf16"),     # ragged M, N and K tiles
     (70, 384, 128, 128, 4, "bf16"),
