@@ -96,12 +96,20 @@ int qmm_n_split(int m, int n, int k, int cu_count);
 size_t qmm_n_scratch_bytes(int m, int n, int split);
 hipError_t launch_qmm_n(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k, int split,
                         float* partial);
-// Decode (M = 1) transpose=false at 4/8 bits on the VALU; parts > 1 splits K
-// into fp32 partials (parts * N floats) added in order by a second kernel.
+// Decode (M = 1) transpose=false at 4/8 bits on the VALU: rows per thread
+// and step, K parts and the split-K scratch they need (arrival words at the
+// head, zero between launches, then fp32 sums); parts == 1 needs none.
+// qvm_plan never asks for more than scratch_cap.
 bool qvm_fits(const QuantArgs& q, int n, int k);
-int qvm_parts(int n, int k, int cu_count);
-hipError_t launch_qvm(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k, int parts,
-                      float* partial);
+struct QvmPlan {
+  int rpt;
+  int parts;
+  int k_part;
+  size_t scratch_bytes;
+};
+QvmPlan qvm_plan(const QuantArgs& q, int n, int k, int cu_count, size_t scratch_cap);
+hipError_t launch_qvm(hipStream_t s, const QvmPlan& p, void* scratch, const QuantArgs& q, const void* x, void* y,
+                      int n, int k);
 // Routed-expert plumbing (kernels/moe.hip): top-k routing, stable sort of
 // (token, slot) rows by expert, weighted combine back to tokens.
 size_t moe_sort_scratch_bytes(int rows, int n_experts);

@@ -555,18 +555,14 @@ cpq_status cpq_affine_qmm_n(cpq_commands* cmds, cpq_dtype dtype, const uint32_t*
   if (st != CPQ_OK) return st;
   cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
   if (m == 1 && k > 0 && (reinterpret_cast<uintptr_t>(x) & 3u) == 0 && cpq::qvm_fits(q, (int)n, (int)k)) {
-    // Decode (qvm): the VALU kernel, K split into partials in session scratch
-    // when it holds them.
-    int parts = cpq::qvm_parts((int)n, (int)k, cmds->dev ? cmds->dev->cu_count : 0);
-    float* partial = nullptr;
-    if (parts > 1) {
-      void* scratch = nullptr;
-      if (cpq::session_scratch(cmds, cpq::kWideCounterBytes + (size_t)parts * n * 4, &scratch))
-        partial = reinterpret_cast<float*>(static_cast<char*>(scratch) + cpq::kWideCounterBytes);
-      else
-        parts = 1;
-    }
-    return cpq::launched(cpq::launch_qvm(cmds->stream, q, x, y, (int)n, (int)k, parts, partial), "affine_qvm launch");
+    // Decode (qvm): the VALU kernel, K split over parts that meet in the
+    // session scratch when it holds them (the plan depends on the session's
+    // fixed capacity only).
+    const cpq::QvmPlan plan = cpq::qvm_plan(q, (int)n, (int)k, cmds->dev ? cmds->dev->cu_count : 0,
+                                            cmds->scratch ? cmds->scratch_bytes : 0);
+    void* scratch = nullptr;
+    if (plan.scratch_bytes) cpq::session_scratch(cmds, plan.scratch_bytes, &scratch);
+    return cpq::launched(cpq::launch_qvm(cmds->stream, plan, scratch, q, x, y, (int)n, (int)k), "affine_qvm launch");
   }
   // Few output tiles: split K into fp32 partials in session scratch (past the
   // prefill kernel's counters) when the session's scratch holds them, else

@@ -82,3 +82,76 @@ def test_qmm_n_zero_k_writes_zeros(device):
                                            _ptr(Y), 3 * 64, 3, 64, 0, 64, 4))
     cmds.commit_and_wait()
     assert not Y.to_numpy()[: 3 * 64].any()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rpt,parts", [(2, 1), (4, 3), (4, 16), (2, 64), (4, 5)])
+def test_qvm_plans(device, library, oracle, monkeypatch, rpt, parts):
+    """Every rows-per-thread step and K split of the decode kernel (forced
+    through its tuning hooks) meets the tolerance, and repeated calls give
+    identical bits: parts are added in part order whatever order they
+    arrive in."""
+    from cider_press_amd.kernels import qmm as kqmm
+
+    monkeypatch.setenv("CPQ_QVM_RPT", str(rpt))
+    monkeypatch.setenv("CPQ_QVM_PARTS", str(parts))
+    n, k, gs, bits = 2080, 4000, 32, 4 if parts != 1 else 8
+    rng = np.random.default_rng(rpt * 100 + parts)
+    w_q, s, b = make_weight(rng, k, n, gs, bits, "bf16")
+    x = make_x(rng, 1, k, "bf16")
+    W, S, B, X = (device.upload(w_q.reshape(-1), "u32"), device.upload(s.reshape(-1), "bf16"),
+                  device.upload(b.reshape(-1), "bf16"), device.upload(x.reshape(-1), "bf16"))
+    cmds = device.commands()
+    ys = []
+    for _ in range(3):
+        Y = device.alloc_buffer(n, "bf16")
+        kqmm.affine_qvm(cmds, library, W, S, B, X, Y, k, n, gs, bits)
+        ys.append(Y)
+    cmds.commit_and_wait()
+    ys = [y.to_numpy()[:n] for y in ys]
+    for y in ys[1:]:
+        assert np.array_equal(y, ys[0])
+    wd = from_bits(oracle.dequantize(w_q, s, b, k, n, gs, bits, "bf16"), "bf16").astype(np.float64).reshape(k, n)
+    ref = from_bits(x, "bf16").astype(np.float64).reshape(1, k) @ wd
+    rep = oracle.tolerance_report(ys[0].reshape(1, n), ref, x, k, "bf16")
+    assert rep["ok"], rep
+
+
+@pytest.mark.gpu
+def test_qvm_graph_replay_and_shared_counters(device, library, oracle):
+    """qvm launches captured in a graph replay bit-equal to eager calls, and
+    qvm and split-K small-M launches back to back on one session leave the
+    shared arrival words zero for each other."""
+    from cider_press_amd.kernels import qmm as kqmm
+
+    rng = np.random.default_rng(5)
+    n, k, gs = 4096, 4096, 64
+    w_q, s, b = make_weight(rng, k, n, gs, 4, "bf16")
+    x = make_x(rng, 1, k, "bf16")
+    W, S, B, X = (device.upload(w_q.reshape(-1), "u32"), device.upload(s.reshape(-1), "bf16"),
+                  device.upload(b.reshape(-1), "bf16"), device.upload(x.reshape(-1), "bf16"))
+    mw, ms, mb = make_weight(rng, 4096, 4096, 64, 4, "bf16")  # small-M operand, [N, K]
+    mx = make_x(rng, 64, 4096, "bf16")
+    MW, MS, MB, MX = (device.upload(mw.reshape(-1), "u32"), device.upload(ms.reshape(-1), "bf16"),
+                      device.upload(mb.reshape(-1), "bf16"), device.upload(mx.reshape(-1), "bf16"))
+    cmds = device.commands()
+    Y0 = device.alloc_buffer(n, "bf16")
+    kqmm.affine_qvm(cmds, library, W, S, B, X, Y0, k, n, gs, 4)
+    cmds.commit_and_wait()
+    y0 = Y0.to_numpy()[:n]
+    Y, MY = device.alloc_buffer(n, "bf16"), device.alloc_buffer(64 * 4096, "bf16")
+    cmds.begin_capture()
+    kqmm.affine_qvm(cmds, library, W, S, B, X, Y, k, n, gs, 4)
+    kqmm.quantized_matmul(cmds, MW, MS, MB, MX, MY, 64, 4096, 4096, 64, 4)
+    kqmm.affine_qvm(cmds, library, W, S, B, X, Y, k, n, gs, 4)
+    graph = cmds.end_capture()
+    mref = oracle.qmm_ref(mx, mw, ms, mb, 64, 4096, 4096, 64, 4, "bf16")
+    for _ in range(3):
+        Y.write(np.zeros(n, np.uint16))
+        graph.launch(cmds)
+        cmds.commit_and_wait()
+        assert np.array_equal(Y.to_numpy()[:n], y0)
+        assert oracle.tolerance_report(MY.to_numpy().reshape(64, 4096), mref, mx, 4096, "bf16")["ok"]
+    wd = from_bits(oracle.dequantize(w_q, s, b, k, n, gs, 4, "bf16"), "bf16").astype(np.float64).reshape(k, n)
+    ref = from_bits(x, "bf16").astype(np.float64).reshape(1, k) @ wd
+    assert oracle.tolerance_report(y0.reshape(1, n), ref, x, k, "bf16")["ok"]
