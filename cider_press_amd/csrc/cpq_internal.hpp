@@ -127,6 +127,27 @@ hipError_t launch_embed(hipStream_t s, const QuantArgs& q, const uint32_t* ids, 
 
 // Decode GEMV: y[N] = x[K] . W^T for one activation row.
 hipError_t launch_qmv(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k);
+
+// A batch folded into a grid dimension (MLX's adjust_matrix_offsets):
+// element z (row-major over shape[0..nd)) takes its operands at
+// sum_d idx_d(z) * st[o][d] elements (o: w_q in u32 words, scales, biases,
+// x in T elements) and writes its output block at z * (block size).
+constexpr int kMaxBatchDims = 8;
+struct BatchArgs {
+  int nd;
+  int shape[kMaxBatchDims];
+  long long st[4][kMaxBatchDims];
+};
+// The decode kernel with the batch in its grid (4/8-bit, gs 32/64/128,
+// K a multiple of 2048 up to 16384; every element's scales and biases
+// 8-byte aligned): whether it takes the shape, and the launch.
+bool qmv_batch_fits(const QuantArgs& q, int n, int k);
+hipError_t launch_qmv_batched(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k, int count,
+                              const BatchArgs& ba);
+// The decode layout for up to 16 rows with the batch in its grid (shape
+// limits of qmv_rows_fits, for every element).
+hipError_t launch_qmv_rows_batched(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
+                                   int count, const BatchArgs& ba);
 // The decode layout for up to 16 rows: Y[M, N] = X[M, K] . W^T (shape limits
 // in qmv_rows_fits).
 bool qmv_rows_fits(const QuantArgs& q, int m, int n, int k, const void* x);

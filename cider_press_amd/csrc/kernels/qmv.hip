@@ -349,12 +349,37 @@ __device__ __forceinline__ f32x4 lean_stream(__amdgpu_buffer_rsrc_t wr, uint32_t
   return acc;
 }
 
-template <typename TT, int BITS, int GS_SHIFT, int WAVES, int PF, bool ONE>
+// Batch element z's operands (the batch in grid dimension y): indices over
+// the batch shape, innermost dimension last, times each operand's element
+// strides; the output block of element z follows the z blocks before it.
+template <typename W, typename S, typename X, typename Y>
+__device__ __forceinline__ void batch_operands(const BatchArgs& ba, uint32_t z, W& w, S& scales, S& biases, X& x,
+                                               Y& y, size_t y_block) {
+  y += (size_t)z * y_block;
+  long long o[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int d = kMaxBatchDims - 1; d >= 0; --d)
+    if (d < ba.nd) {
+      const uint32_t sh = (uint32_t)ba.shape[d];
+      const long long i = (long long)(z % sh);
+      z /= sh;
+#pragma unroll
+      for (int op = 0; op < 4; ++op) o[op] += i * ba.st[op][d];
+    }
+  w += o[0];
+  scales += o[1];
+  biases += o[2];
+  x += o[3];
+}
+
+template <typename TT, int BITS, int GS_SHIFT, int WAVES, int PF, bool ONE, bool BATCH>
 __global__ __launch_bounds__(64 * WAVES) void qmv_lean_kernel(const uint32_t* __restrict__ w,
                                                                    const uint16_t* __restrict__ scales,
                                                                    const uint16_t* __restrict__ biases,
                                                                    const uint16_t* __restrict__ x,
-                                                                   uint16_t* __restrict__ y, int n, int k) {
+                                                                   uint16_t* __restrict__ y, int n, int k,
+                                                                   const BatchArgs ba) {
+  if constexpr (BATCH) batch_operands(ba, blockIdx.y, w, scales, biases, x, y, (size_t)n);
   constexpr int CB = BITS * 4;
   constexpr int GPS = 128 >> GS_SHIFT;  // groups per step (4 chunks of 32)
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -475,12 +500,14 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_lean_kernel(const uint32_t* __
 // past M are not read: their A rows only feed output rows that are never
 // stored.  NST steps per wave (K = 128 * WAVES * NST); at most 16
 // activation items per lane (M * NST <= 64).
-template <typename TT, int BITS, int GS_SHIFT, int WAVES, int NST>
+template <typename TT, int BITS, int GS_SHIFT, int WAVES, int NST, bool BATCH>
 __global__ __launch_bounds__(64 * WAVES) void qmm_lean_rows_kernel(const uint32_t* __restrict__ w,
                                                                     const uint16_t* __restrict__ scales,
                                                                     const uint16_t* __restrict__ biases,
                                                                     const uint16_t* __restrict__ x,
-                                                                    uint16_t* __restrict__ y, int m, int n, int k) {
+                                                                    uint16_t* __restrict__ y, int m, int n, int k,
+                                                                    const BatchArgs ba) {
+  if constexpr (BATCH) batch_operands(ba, blockIdx.y, w, scales, biases, x, y, (size_t)m * n);
   constexpr int CB = BITS * 4;
   constexpr int GPS = 128 >> GS_SHIFT;
   constexpr int XMAX = 16;             // activation items per lane
@@ -653,12 +680,12 @@ hipError_t launch_pf(hipStream_t s, const QuantArgs& q, const void* x, void* y, 
   return launch_cfg<TT, BITS, WAVES, PF, false>(s, q, x, y, n, k, lds);
 }
 
-template <typename TT, int BITS, int GS_SHIFT, int WAVES, int PF, bool ONE>
+template <typename TT, int BITS, int GS_SHIFT, int WAVES, int PF, bool ONE, bool BATCH = false>
 hipError_t launch_lean_cfg(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k,
-                           size_t lds) {
+                           size_t lds, int count, const BatchArgs& ba) {
   if (lds > 64 * 1024) {
     static const hipError_t attr = [] {
-      const void* fn = reinterpret_cast<const void*>(&qmv_lean_kernel<TT, BITS, GS_SHIFT, WAVES, PF, ONE>);
+      const void* fn = reinterpret_cast<const void*>(&qmv_lean_kernel<TT, BITS, GS_SHIFT, WAVES, PF, ONE, BATCH>);
       hipFuncAttributes fa;
       hipError_t e = hipFuncGetAttributes(&fa, fn);
       if (e != hipSuccess) return e;
@@ -667,29 +694,30 @@ hipError_t launch_lean_cfg(hipStream_t s, const QuantArgs& q, const void* x, voi
     }();
     if (attr != hipSuccess) return attr;
   }
-  hipLaunchKernelGGL((qmv_lean_kernel<TT, BITS, GS_SHIFT, WAVES, PF, ONE>), dim3((unsigned)((n + 15) / 16)),
-                     dim3(64 * WAVES), lds, s, q.w, static_cast<const uint16_t*>(q.scales),
-                     static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x),
-                     static_cast<uint16_t*>(y), n, k);
+  hipLaunchKernelGGL((qmv_lean_kernel<TT, BITS, GS_SHIFT, WAVES, PF, ONE, BATCH>),
+                     dim3((unsigned)((n + 15) / 16), (unsigned)count), dim3(64 * WAVES), lds, s, q.w,
+                     static_cast<const uint16_t*>(q.scales), static_cast<const uint16_t*>(q.biases),
+                     static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), n, k, ba);
   return hipGetLastError();
 }
 
-template <typename TT, int BITS, int GS_SHIFT, int WAVES>
+template <typename TT, int BITS, int GS_SHIFT, int WAVES, bool BATCH = false>
 hipError_t launch_lean_gs(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k,
-                          size_t lds) {
+                          size_t lds, int count = 1, const BatchArgs& ba = BatchArgs{}) {
   const int nsteps = k / (128 * WAVES);
-  if (nsteps == 8) return launch_lean_cfg<TT, BITS, GS_SHIFT, WAVES, 8, true>(s, q, x, y, n, k, lds);
-  if (nsteps == 4) return launch_lean_cfg<TT, BITS, GS_SHIFT, WAVES, 4, true>(s, q, x, y, n, k, lds);
-  if (nsteps % 8 == 0) return launch_lean_cfg<TT, BITS, GS_SHIFT, WAVES, 8, false>(s, q, x, y, n, k, lds);
-  return launch_lean_cfg<TT, BITS, GS_SHIFT, WAVES, 4, false>(s, q, x, y, n, k, lds);
+  if (nsteps == 8) return launch_lean_cfg<TT, BITS, GS_SHIFT, WAVES, 8, true, BATCH>(s, q, x, y, n, k, lds, count, ba);
+  if (nsteps == 4) return launch_lean_cfg<TT, BITS, GS_SHIFT, WAVES, 4, true, BATCH>(s, q, x, y, n, k, lds, count, ba);
+  if (nsteps % 8 == 0)
+    return launch_lean_cfg<TT, BITS, GS_SHIFT, WAVES, 8, false, BATCH>(s, q, x, y, n, k, lds, count, ba);
+  return launch_lean_cfg<TT, BITS, GS_SHIFT, WAVES, 4, false, BATCH>(s, q, x, y, n, k, lds, count, ba);
 }
 
-template <typename TT, int BITS, int WAVES>
+template <typename TT, int BITS, int WAVES, bool BATCH = false>
 hipError_t launch_lean_w(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k,
-                         size_t lds) {
-  if (q.gs == 32) return launch_lean_gs<TT, BITS, 5, WAVES>(s, q, x, y, n, k, lds);
-  if (q.gs == 64) return launch_lean_gs<TT, BITS, 6, WAVES>(s, q, x, y, n, k, lds);
-  return launch_lean_gs<TT, BITS, 7, WAVES>(s, q, x, y, n, k, lds);
+                         size_t lds, int count = 1, const BatchArgs& ba = BatchArgs{}) {
+  if (q.gs == 32) return launch_lean_gs<TT, BITS, 5, WAVES, BATCH>(s, q, x, y, n, k, lds, count, ba);
+  if (q.gs == 64) return launch_lean_gs<TT, BITS, 6, WAVES, BATCH>(s, q, x, y, n, k, lds, count, ba);
+  return launch_lean_gs<TT, BITS, 7, WAVES, BATCH>(s, q, x, y, n, k, lds, count, ba);
 }
 
 // The lean kernel's shape contract: K a multiple of 512 * waves (each wave a
@@ -706,12 +734,12 @@ bool lean_fits(const QuantArgs& q, int n, int k, int waves) {
   return ((reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases)) & 7u) == 0;
 }
 
-template <typename TT, int BITS, int GS_SHIFT, int NST>
+template <typename TT, int BITS, int GS_SHIFT, int NST, bool BATCH>
 hipError_t launch_rows_cfg(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
-                           size_t lds) {
+                           size_t lds, int count, const BatchArgs& ba) {
   if (lds > 64 * 1024) {
     static const hipError_t attr = [] {
-      const void* fn = reinterpret_cast<const void*>(&qmm_lean_rows_kernel<TT, BITS, GS_SHIFT, 8, NST>);
+      const void* fn = reinterpret_cast<const void*>(&qmm_lean_rows_kernel<TT, BITS, GS_SHIFT, 8, NST, BATCH>);
       hipFuncAttributes fa;
       hipError_t e = hipFuncGetAttributes(&fa, fn);
       if (e != hipSuccess) return e;
@@ -720,19 +748,20 @@ hipError_t launch_rows_cfg(hipStream_t s, const QuantArgs& q, const void* x, voi
     }();
     if (attr != hipSuccess) return attr;
   }
-  hipLaunchKernelGGL((qmm_lean_rows_kernel<TT, BITS, GS_SHIFT, 8, NST>), dim3((unsigned)((n + 15) / 16)), dim3(512),
-                     lds, s, q.w, static_cast<const uint16_t*>(q.scales), static_cast<const uint16_t*>(q.biases),
-                     static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), m, n, k);
+  hipLaunchKernelGGL((qmm_lean_rows_kernel<TT, BITS, GS_SHIFT, 8, NST, BATCH>),
+                     dim3((unsigned)((n + 15) / 16), (unsigned)count), dim3(512), lds, s, q.w,
+                     static_cast<const uint16_t*>(q.scales), static_cast<const uint16_t*>(q.biases),
+                     static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), m, n, k, ba);
   return hipGetLastError();
 }
 
-template <typename TT, int BITS, int GS_SHIFT>
+template <typename TT, int BITS, int GS_SHIFT, bool BATCH>
 hipError_t launch_rows_gs(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
-                          size_t lds) {
+                          size_t lds, int count, const BatchArgs& ba) {
   const int nst = k / 1024;
-  if (nst == 4) return launch_rows_cfg<TT, BITS, GS_SHIFT, 4>(s, q, x, y, m, n, k, lds);
-  if (nst == 8) return launch_rows_cfg<TT, BITS, GS_SHIFT, 8>(s, q, x, y, m, n, k, lds);
-  return launch_rows_cfg<TT, BITS, GS_SHIFT, 16>(s, q, x, y, m, n, k, lds);
+  if (nst == 4) return launch_rows_cfg<TT, BITS, GS_SHIFT, 4, BATCH>(s, q, x, y, m, n, k, lds, count, ba);
+  if (nst == 8) return launch_rows_cfg<TT, BITS, GS_SHIFT, 8, BATCH>(s, q, x, y, m, n, k, lds, count, ba);
+  return launch_rows_cfg<TT, BITS, GS_SHIFT, 16, BATCH>(s, q, x, y, m, n, k, lds, count, ba);
 }
 
 size_t rows_lds(int m, int k, int gs) {
@@ -814,20 +843,52 @@ bool qmv_rows_fits(const QuantArgs& q, int m, int n, int k, const void* x) {
          (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
 }
 
-hipError_t launch_qmv_rows(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k) {
+template <bool BATCH>
+hipError_t launch_rows_any(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k, int count,
+                           const BatchArgs& ba) {
   const size_t lds = rows_lds(m, k, q.gs);
   auto by_gs = [&](auto tt, auto bits) -> hipError_t {
     using TT = decltype(tt);
     constexpr int B = decltype(bits)::value;
-    if (q.gs == 32) return launch_rows_gs<TT, B, 5>(s, q, x, y, m, n, k, lds);
-    if (q.gs == 64) return launch_rows_gs<TT, B, 6>(s, q, x, y, m, n, k, lds);
-    return launch_rows_gs<TT, B, 7>(s, q, x, y, m, n, k, lds);
+    if (q.gs == 32) return launch_rows_gs<TT, B, 5, BATCH>(s, q, x, y, m, n, k, lds, count, ba);
+    if (q.gs == 64) return launch_rows_gs<TT, B, 6, BATCH>(s, q, x, y, m, n, k, lds, count, ba);
+    return launch_rows_gs<TT, B, 7, BATCH>(s, q, x, y, m, n, k, lds, count, ba);
   };
   using B4 = std::integral_constant<int, 4>;
   using B8 = std::integral_constant<int, 8>;
   if (q.dtype == CPQ_DTYPE_BF16) return q.bits == 4 ? by_gs(BF16{}, B4{}) : by_gs(BF16{}, B8{});
   if (q.dtype == CPQ_DTYPE_F16) return q.bits == 4 ? by_gs(F16{}, B4{}) : by_gs(F16{}, B8{});
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_qmv_rows(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k) {
+  return launch_rows_any<false>(s, q, x, y, m, n, k, 1, BatchArgs{});
+}
+
+hipError_t launch_qmv_rows_batched(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
+                                   int count, const BatchArgs& ba) {
+  if (count < 1 || count > 65535) return hipErrorInvalidValue;
+  return launch_rows_any<true>(s, q, x, y, m, n, k, count, ba);
+}
+
+// The batched decode kernel runs 4 waves per workgroup (the batch fills the
+// grid): the lean kernel's contract at 4 waves, LDS within the CU.
+bool qmv_batch_fits(const QuantArgs& q, int n, int k) {
+  if (q.dtype != CPQ_DTYPE_BF16 && q.dtype != CPQ_DTYPE_F16) return false;
+  const bool fits = q.bits == 4 ? lean_fits<4>(q, n, k, 4) : q.bits == 8 ? lean_fits<8>(q, n, k, 4) : false;
+  if (!fits) return false;
+  return (size_t)4 * lean_wave_lds(k / 512, shift_of(q.gs)) + (size_t)4 * 16 * 4 <= 160 * 1024 - 1024;
+}
+
+hipError_t launch_qmv_batched(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k, int count,
+                              const BatchArgs& ba) {
+  if (count < 1 || count > 65535 || !qmv_batch_fits(q, n, k)) return hipErrorInvalidValue;
+  const size_t lds = (size_t)4 * lean_wave_lds(k / 512, shift_of(q.gs)) + (size_t)4 * 16 * 4;
+  if (q.dtype == CPQ_DTYPE_BF16)
+    return q.bits == 4 ? launch_lean_w<BF16, 4, 4, true>(s, q, x, y, n, k, lds, count, ba)
+                       : launch_lean_w<BF16, 8, 4, true>(s, q, x, y, n, k, lds, count, ba);
+  return q.bits == 4 ? launch_lean_w<F16, 4, 4, true>(s, q, x, y, n, k, lds, count, ba)
+                     : launch_lean_w<F16, 8, 4, true>(s, q, x, y, n, k, lds, count, ba);
 }
 
 hipError_t launch_qmv(hipStream_t s, const QuantArgs& q, const void* x, void* y, int n, int k) {

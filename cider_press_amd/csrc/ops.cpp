@@ -395,6 +395,43 @@ cpq_status cpq_affine_qmm_t(cpq_commands* cmds, cpq_dtype dtype, const uint32_t*
   return cpq::launched(cpq::launch_session_qmm(cmds, q, x, y, (int)m, (int)n, (int)k), "affine_qmm_t launch");
 }
 
+namespace cpq {
+namespace {
+
+// Y[M, N] = X[M, K] . W^T for M > 1 on validated operands: the kernel the
+// shape runs best on.  Up to 16 rows at K = 4096 / 8192 / 16384 (4/8-bit):
+// the decode kernel's layout with M activation rows.  Other small-M 4/8-bit
+// shapes with K a multiple of 256: the tiled small-M kernel.  Other small-M
+// shapes: the slab kernel.  Larger M: the prefill plan.  CPQ_SMALL_M=0
+// forces the slab kernel, CPQ_QMV_ROWS=0 skips the decode layout (tuning
+// hooks, read once per process).
+cpq_status route_matmul(cpq_commands* cmds, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
+                        const char* op) {
+  const std::string what = std::string(op) + (m <= skinny_max_m(q, n, k) ? " (small-M) launch" : " (prefill) launch");
+  if (m <= skinny_max_m(q, n, k)) {
+    static const bool small_on = [] {
+      const char* e = std::getenv("CPQ_SMALL_M");
+      return !(e && *e == '0');
+    }();
+    const bool words4 = ((reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases)) & 3u) == 0;
+    const SmallPlan sp = small_on && aligned16(x) && aligned16(q.w) && words4
+                             ? qmm_small_plan(q, m, n, k, cmds->dev->cu_count, cmds->scratch ? cmds->scratch_bytes : 0)
+                             : SmallPlan{0, 0, 0, 0, 0};
+    static const bool rows_on = [] {
+      const char* e = std::getenv("CPQ_QMV_ROWS");
+      return !(e && *e == '0');
+    }();
+    if (small_on && rows_on && qmv_rows_fits(q, m, n, k, x))
+      return launched(launch_qmv_rows(cmds->stream, q, x, y, m, n, k), what.c_str());
+    if (sp.split > 0) return launched(launch_qmm_small(cmds->stream, sp, cmds->scratch, q, x, y, m, n, k), what.c_str());
+    return launched(launch_qmm_skinny(cmds->stream, q, x, y, m, n, k), what.c_str());
+  }
+  return launched(launch_session_qmm(cmds, q, x, y, m, n, k), what.c_str());
+}
+
+}  // namespace
+}  // namespace cpq
+
 // ---------------------------------------------------------------------------
 // Batched forms (MLX's `batched` kernels, adjust_matrix_offsets in
 // quantized.h:1351-1388): batch element z picks its x, w, scales and biases
@@ -404,7 +441,7 @@ cpq_status cpq_affine_qmm_t(cpq_commands* cmds, cpq_dtype dtype, const uint32_t*
 
 namespace {
 
-constexpr int kMaxBatchDims = 8;
+using cpq::kMaxBatchDims;
 
 int64_t batch_offset(size_t z, int nd, const int* shape, const int64_t* st) {
   int64_t off = 0;
@@ -452,6 +489,41 @@ cpq_status check_batch(const char* op, int nd, const int* shape, const int64_t* 
   return CPQ_OK;
 }
 
+// No weight operand (w_q, scales, biases) moves along the batch.
+bool weights_shared(int nd, const int* shape, const int64_t* const st[4]) {
+  for (int d = 0; d < nd; ++d)
+    if (shape[d] > 1 && (st[0][d] || st[1][d] || st[2][d])) return false;
+  return true;
+}
+
+// Element z's activations start at z * block: the batch of x is one dense
+// row-major array of blocks.
+bool x_dense(int nd, const int* shape, const int64_t* xst, size_t block) {
+  uint64_t span = block;
+  for (int d = nd - 1; d >= 0; --d) {
+    if (shape[d] > 1 && (uint64_t)xst[d] != span) return false;
+    span *= (uint64_t)shape[d];
+  }
+  return true;
+}
+
+// The batch as kernel arguments; false when an element's scales or biases
+// would lose the 8-byte alignment the decode-layout kernels load with, or
+// the batch does not fit a grid dimension.
+bool batch_args(int nd, const int* shape, const int64_t* const st[4], size_t count, const void* scales,
+                const void* biases, cpq::BatchArgs* ba) {
+  if (count > 65535) return false;
+  if (((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(biases)) & 7u) != 0) return false;
+  *ba = cpq::BatchArgs{};
+  ba->nd = nd;
+  for (int d = 0; d < nd; ++d) {
+    if (st[1][d] % 4 || st[2][d] % 4) return false;
+    ba->shape[d] = shape[d];
+    for (int o = 0; o < 4; ++o) ba->st[o][d] = st[o][d];
+  }
+  return true;
+}
+
 }  // namespace
 
 cpq_status cpq_affine_qmm_t_batched(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q, size_t w_q_len,
@@ -477,7 +549,24 @@ cpq_status cpq_affine_qmm_t_batched(cpq_commands* cmds, cpq_dtype dtype, const u
   size_t ylen;
   if (!cpq::mul_ok(count, mn, &ylen) || y_len != ylen)
     return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmm_t_batched: y.len() != batch*M*N");
+  if (count == 0 || mn == 0) return CPQ_OK;
   const size_t esz = cpq::dtype_size(dtype);
+  st = cpq::check_ptrs("affine_qmm_t_batched", w_q, scales, biases, x, y);
+  if (st != CPQ_OK) return st;
+  const cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
+  if (count > 1 && weights_shared(batch_ndims, batch_shape, strides) &&
+      x_dense(batch_ndims, batch_shape, x_strides, mk) && count * m <= (size_t)INT32_MAX) {
+    // One weight for every element and the activations one dense array:
+    // a single matmul over count * M rows (the weights are read once).
+    return cpq::route_matmul(cmds, q, x, y, (int)(count * m), (int)n, (int)k, "affine_qmm_t_batched");
+  }
+  cpq::BatchArgs ba;
+  if (count > 1 && m <= 16 && cpq::qmv_rows_fits(q, (int)m, (int)n, (int)k, x) &&
+      batch_args(batch_ndims, batch_shape, strides, count, scales, biases, &ba)) {
+    // Few rows per element: the decode layout with the batch in its grid.
+    return cpq::launched(cpq::launch_qmv_rows_batched(cmds->stream, q, x, y, (int)m, (int)n, (int)k, (int)count, ba),
+                         "affine_qmm_t_batched launch");
+  }
   for (size_t z = 0; z < count; ++z) {
     const uint32_t* wz = w_q + batch_offset(z, batch_ndims, batch_shape, w_strides);
     const char* sz = static_cast<const char*>(scales) + batch_offset(z, batch_ndims, batch_shape, s_strides) * esz;
@@ -513,6 +602,23 @@ cpq_status cpq_affine_qmv_batched(cpq_commands* cmds, cpq_dtype dtype, const uin
   size_t ylen;
   if (!cpq::mul_ok(count, n, &ylen) || y_len != ylen)
     return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_qmv_batched: y.len() != batch*N");
+  if (count == 0 || n == 0) return CPQ_OK;
+  st = cpq::check_ptrs("affine_qmv_batched", w_q, scales, biases, x, y);
+  if (st != CPQ_OK) return st;
+  const cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
+  if (count > 1 && n % 32 == 0 && weights_shared(batch_ndims, batch_shape, strides) &&
+      x_dense(batch_ndims, batch_shape, x_strides, k) && count <= (size_t)INT32_MAX) {
+    // One weight for every element and the activations one dense array:
+    // a single matmul over count rows (the weights are read once).
+    return cpq::route_matmul(cmds, q, x, y, (int)count, (int)n, (int)k, "affine_qmv_batched");
+  }
+  cpq::BatchArgs ba;
+  if (count > 1 && cpq::qmv_batch_fits(q, (int)n, (int)k) &&
+      batch_args(batch_ndims, batch_shape, strides, count, scales, biases, &ba)) {
+    // The decode kernel with the batch in its grid.
+    return cpq::launched(cpq::launch_qmv_batched(cmds->stream, q, x, y, (int)n, (int)k, (int)count, ba),
+                         "affine_qmv_batched launch");
+  }
   for (size_t z = 0; z < count; ++z) {
     const uint32_t* wz = w_q + batch_offset(z, batch_ndims, batch_shape, w_strides);
     const char* sz = static_cast<const char*>(scales) + batch_offset(z, batch_ndims, batch_shape, s_strides) * esz;
@@ -732,37 +838,7 @@ cpq_status cpq_quantized_matmul(cpq_commands* cmds, cpq_dtype dtype, const uint3
   st = cpq::check_ptrs("quantized_matmul", w_q, scales, biases, x, y);
   if (st != CPQ_OK) return st;
   cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
-  if ((long)m <= cpq::skinny_max_m(q, (int)n, (int)k_physical)) {
-    // Up to 16 rows at K = 4096 / 8192 / 16384 (4/8-bit): the decode kernel's
-    // layout with M activation rows.  Other 4/8-bit shapes with K a multiple
-    // of 256: the tiled small-M kernel.  Everything else: the slab kernel.
-    // CPQ_SMALL_M=0 forces the slab kernel, CPQ_QMV_ROWS=0 skips the decode
-    // layout (tuning hooks, read once per process).
-    static const bool small_on = [] {
-      const char* e = std::getenv("CPQ_SMALL_M");
-      return !(e && *e == '0');
-    }();
-    const bool words4 = ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(biases)) & 3u) == 0;
-    const cpq::SmallPlan sp = small_on && cpq::aligned16(x) && cpq::aligned16(w_q) && words4
-                                  ? cpq::qmm_small_plan(q, (int)m, (int)n, (int)k_physical, cmds->dev->cu_count,
-                                                        cmds->scratch ? cmds->scratch_bytes : 0)
-                                  : cpq::SmallPlan{0, 0, 0, 0, 0};
-    static const bool rows_on = [] {
-      const char* e = std::getenv("CPQ_QMV_ROWS");
-      return !(e && *e == '0');
-    }();
-    if (small_on && rows_on && cpq::qmv_rows_fits(q, (int)m, (int)n, (int)k_physical, x))
-      return cpq::launched(cpq::launch_qmv_rows(cmds->stream, q, x, y, (int)m, (int)n, (int)k_physical),
-                           "quantized_matmul (small-M) launch");
-    if (sp.split > 0)
-      return cpq::launched(
-          cpq::launch_qmm_small(cmds->stream, sp, cmds->scratch, q, x, y, (int)m, (int)n, (int)k_physical),
-          "quantized_matmul (small-M) launch");
-    return cpq::launched(cpq::launch_qmm_skinny(cmds->stream, q, x, y, (int)m, (int)n, (int)k_physical),
-                         "quantized_matmul (small-M) launch");
-  }
-  return cpq::launched(cpq::launch_session_qmm(cmds, q, x, y, (int)m, (int)n, (int)k_physical),
-                       "quantized_matmul (prefill) launch");
+  return cpq::route_matmul(cmds, q, x, y, (int)m, (int)n, (int)k_physical, "quantized_matmul");
 }
 
 }  // extern "C"
