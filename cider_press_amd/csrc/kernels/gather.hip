@@ -7,21 +7,32 @@
 //
 // A workgroup (8 waves) owns one expert and one chunk of NC output columns.
 // Per pass it gathers up to R = 16*MB of the rows routed to its expert (in row
-// order: sorted routing by binary search, unsorted by per-64-row-block match
-// counts, their prefix, and a ballot placement), stages those rows'
-// activations in LDS once (16-byte chunks XOR-swizzled by row, conflict-free
-// for the MFMA reads), and then streams the chunk's weights:
+// order: sorted routing by counting the rows below / at the expert in one
+// pass, unsorted by per-64-row-block match counts, their prefix, and a ballot
+// placement), stages those rows' activations in LDS once, and then streams
+// the chunk's weights:
 //   - wave w owns the 16-column slabs w, w+8, ... of the chunk; for each slab
-//     it walks K in steps of 4 chunks (lane l: column l%16, chunk 4u + l/16),
-//     4 steps of weights and their (scale, bias) in flight;
-//   - each step is dequantized in registers (natural k order; the exact
-//     single-FMA form when every lane's group allows it, else fmaf) into four
-//     v_mfma_f32_16x16x32 B operands and multiplied against the MB 16-row
-//     activation blocks read from LDS;
-//   - at a slab's last step the 16 x R tile is stored.
-// Weights stream from HBM exactly once per pass and activations are read
-// from L2 once per workgroup, so the kernel runs at the weight stream's rate
-// for routings with up to R rows per expert (more rows: more passes).
+//     it walks K in units of 4 chunks (lane l: column l%16, chunk 4u + l/16);
+//     the unit's weights, (scale, bias) words and LDS offsets move by
+//     wave-uniform amounts, so the loads take them in the scalar offset and
+//     the step costs no address arithmetic beyond one add per LDS read;
+//   - weights run 4 steps ahead of use and (scale, bias) words 4 to 8 steps
+//     ahead, in register rings indexed by the unrolled step (no copies);
+//   - each step is dequantized in registers (the exact single-FMA form when
+//     the packed exponent check clears the wave's (scale, bias) words of the
+//     load, else fmaf; the same bits either way) into four
+//     v_mfma_f32_16x16x32 B operands and multiplied against the pass's
+//     16-row activation blocks read from LDS;
+//   - at a slab's last step its 16 x R tile is stored.
+// The routing, the pass's activation rows and their loads go first (three
+// dependent round trips on a memory system not yet loaded by the stream);
+// the first weight steps are requested right after the activation loads.
+// Activation layout in LDS: [unit][16-row block][row][16 slots of 16 bytes],
+// slot s of row i stored at slot s ^ (i % 16) (the 16 rows of an MFMA read 16
+// distinct slots).  Weights stream from HBM exactly once per pass and
+// activations are read from L2 once per workgroup, so the kernel runs at the
+// weight stream's rate for routings with up to R rows per expert (more rows:
+// more passes).
 #include <algorithm>
 
 #include "../cpq_internal.hpp"
@@ -34,9 +45,12 @@ using namespace dev;
 
 constexpr int GX_WAVES = 8;
 constexpr int GX_THREADS = 64 * GX_WAVES;
-constexpr int GX_PF = 4;                   // steps in flight per wave (4 measured ~2 % faster than 8, 12 slower)
+constexpr int GX_PF = 4;                   // weight steps in flight per wave
+constexpr int GX_UNROLL = 8;               // steps per loop iteration: two turns of the weight ring
 constexpr int GX_XBYTES = 128 * 1024;      // LDS for the staged activation rows
 constexpr int GX_MAXBLK = 1024;            // 64-row routing blocks (n_rows <= 65536)
+constexpr int GX_COUNT_ROWS = 16 * GX_THREADS;  // sorted routing: counted in one pass up to this many rows
+constexpr int GX_XITEMS = GX_XBYTES / 16 / GX_THREADS;  // staged 16-byte items per thread: all of a pass
 
 struct GxShared {
   int cnt[GX_MAXBLK];  // unsorted routing: matches of this expert per 64-row block, then prefix
@@ -45,84 +59,85 @@ struct GxShared {
   int total, lo;
 };
 
-template <int BITS>
-struct GxStep {
-  uint32_t w[BITS];
-  uint32_t s, b;  // kept apart until used: combining them would wait for the loads
-};
-
-// Cursor over a wave's (slab, unit) steps: slab j of the wave is the 16-column
-// slab wave + 8j of the chunk, unit u its chunks 4u .. 4u+3 (lane group g
-// takes 4u + g).  Pointers advance incrementally (no per-step 64-bit math).
-template <int BITS>
-struct GxCursor {
-  const uint32_t* wrow;
-  const uint16_t* srow;
-  const uint16_t* brow;
-  int u, slab, col;
-  __device__ __forceinline__ void next(int units, int my_slabs, size_t wstride, size_t gstride, int n) {
+// A wave's position in its (slab, unit) steps; wave-uniform.
+struct GxPos {
+  int u, j;
+  __device__ __forceinline__ void step(int units) {
     if (++u == units) {
       u = 0;
-      if (slab + 1 < my_slabs) {  // past the last slab: stay (clamped re-loads, never used)
-        ++slab;
-        col += 16 * GX_WAVES;
-        const bool ok = col < n;
-        wrow += ok ? wstride : 0;
-        srow += ok ? gstride : 0;
-        brow += ok ? gstride : 0;
-      }
+      ++j;
+    }
+  }
+  __device__ __forceinline__ void skip(int n, int units) {  // n divides units
+    u += n;
+    if (u == units) {
+      u = 0;
+      ++j;
     }
   }
 };
 
-// Scale / bias words of QS consecutive steps (a "quad"), loaded at its first
-// step when QS > 1: the QS * 128 / GSQ groups of the lane's column that the
-// quad's 4 QS chunks span, in one 8- or 16-byte load each (QS = 1: one 2-byte
-// load of each per step, in the step itself).  The quad's first unit is a
-// multiple of QS, so the vector is aligned and inside the column's row.
-struct GxSb {
-  u32x4 s, b;
-};
-
+// (scale, bias) words per load: QS steps' groups of a lane's column (QS > 1:
+// 16 or 8 bytes, the same for every lane of a column), or one 16-bit group
+// per step (QS = 1).
 template <int QS, int GSQ>
-struct GxQuad {
-  static constexpr int kBytes = QS > 1 ? QS * 128 / GSQ * 2 : 0;
-  static_assert(QS == 1 || kBytes == 8 || kBytes == 16, "quad vector of 8 or 16 bytes");
+struct GxSbw {
+  static constexpr int kWords = QS == 1 ? 1 : QS * 64 / GSQ;
+  static_assert(QS == 1 || kWords == 2 || kWords == 4, "8- or 16-byte (scale, bias) loads");
 };
 
-template <int BITS, int QS>
-__device__ __forceinline__ void gx_load(const GxCursor<BITS>& c, GxStep<BITS>& dst, int chunks, int g,
-                                        int gs_shift) {
-  const int ch = min(4 * c.u + g, chunks - 1);
-  load_chunk<BITS>(c.wrow, (size_t)ch, dst.w);
-  if constexpr (QS == 1) {
-    const int gi = (ch << 5) >> gs_shift;
-    dst.s = c.srow[gi];
-    dst.b = c.brow[gi];
-  }
-}
-
+// Register rings of one wave's stream: weights of GX_PF steps, (scale,
+// bias) words of GX_UNROLL steps.
 template <int BITS, int QS, int GSQ>
-__device__ __forceinline__ void gx_load_sb(const GxCursor<BITS>& c, GxSb& v) {
-  const int gi = (c.u * 128) / GSQ;  // first group of the quad
-  if constexpr (GxQuad<QS, GSQ>::kBytes == 16) {
-    v.s = *reinterpret_cast<const u32x4*>(c.srow + gi);
-    v.b = *reinterpret_cast<const u32x4*>(c.brow + gi);
-  } else {
-    const u32x2 s2 = *reinterpret_cast<const u32x2*>(c.srow + gi);
-    const u32x2 b2 = *reinterpret_cast<const u32x2*>(c.brow + gi);
-    v.s = u32x4{s2[0], s2[1], 0u, 0u};
-    v.b = u32x4{b2[0], b2[1], 0u, 0u};
+struct GxRing {
+  static constexpr int kSb = GX_UNROLL / QS;
+  static constexpr int kW = GxSbw<QS, GSQ>::kWords;
+  uint32_t w[GX_PF][BITS];
+  uint32_t s[kSb][kW], b[kSb][kW];
+};
+
+template <int BITS>
+__device__ __forceinline__ void gx_wload(__amdgpu_buffer_rsrc_t wr, uint32_t voff, uint32_t soff,
+                                         uint32_t (&dst)[BITS]) {
+  static_assert(BITS == 4 || BITS == 8, "4- and 8-bit");
+#pragma unroll
+  for (int q = 0; q < BITS / 4; ++q) {
+    const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff + 16u * q, soff, 0));
+    dst[4 * q] = v.x;
+    dst[4 * q + 1] = v.y;
+    dst[4 * q + 2] = v.z;
+    dst[4 * q + 3] = v.w;
   }
 }
 
-// The 16-bit scale or bias of quad step I for this lane (lane group g): group
-// (128 I + 32 g) / GSQ of the quad.  GSQ = 64: word I, half g / 2 (per lane,
-// `sel` picks it); GSQ = 128: word I / 2, half I % 2.
-// (I is a constant once the step loop is unrolled.)
-template <typename TT, int GSQ>
-__device__ __forceinline__ float gx_sb_f32(const u32x4& v, int I, uint32_t sel) {
-  if constexpr (GSQ == 64) {
+template <int QS, int GSQ, int W>
+__device__ __forceinline__ void gx_sbload(__amdgpu_buffer_rsrc_t sr, __amdgpu_buffer_rsrc_t br, uint32_t voff,
+                                          uint32_t soff, uint32_t (&s)[W], uint32_t (&b)[W]) {
+  if constexpr (W == 4) {
+    const u32x4 sv = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, voff, soff, 0));
+    const u32x4 bv = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(br, voff, soff, 0));
+    s[0] = sv.x; s[1] = sv.y; s[2] = sv.z; s[3] = sv.w;
+    b[0] = bv.x; b[1] = bv.y; b[2] = bv.z; b[3] = bv.w;
+  } else if constexpr (W == 2) {
+    const u32x2 sv = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(sr, voff, soff, 0));
+    const u32x2 bv = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(br, voff, soff, 0));
+    s[0] = sv[0]; s[1] = sv[1];
+    b[0] = bv[0]; b[1] = bv[1];
+  } else {
+    s[0] = __builtin_amdgcn_raw_buffer_load_b16(sr, voff, soff, 0);
+    b[0] = __builtin_amdgcn_raw_buffer_load_b16(br, voff, soff, 0);
+  }
+}
+
+// The 16-bit scale or bias of step I of a load for this lane (lane group g)
+// as f32.  QS = 1: the loaded group.  GSQ = 64: groups 2(u+I) .. +1 of the
+// load's first unit u are word I; this lane's is half g / 2 (`sel`).
+// GSQ = 128: group u + I is word I / 2, half I % 2.
+template <typename TT, int QS, int GSQ, int W>
+__device__ __forceinline__ float gx_sbv(const uint32_t (&v)[W], int I, uint32_t sel) {
+  if constexpr (QS == 1) {
+    return TT::to_f32((uint16_t)v[0]);
+  } else if constexpr (GSQ == 64) {
     const uint32_t word = v[I];
     if constexpr (Sig16<TT>::bf16)
       return __uint_as_float(__builtin_amdgcn_perm(word, word, sel));
@@ -134,7 +149,7 @@ __device__ __forceinline__ float gx_sb_f32(const u32x4& v, int I, uint32_t sel) 
   }
 }
 
-// Byte selector of gx_sb_f32 for lane group g (GSQ = 64): the 16-bit half
+// Byte selector of gx_sbv for lane group g (GSQ = 64): the 16-bit half
 // g / 2 into the high half (bf16: the f32 bits) or the low half (f16).
 template <typename TT>
 __device__ __forceinline__ uint32_t gx_sb_sel(int g) {
@@ -144,18 +159,179 @@ __device__ __forceinline__ uint32_t gx_sb_sel(int g) {
     return (g >> 1) ? 0x0c0c0302u : 0x0c0c0100u;
 }
 
-// The first GX_PF steps of a wave's weight stream; `ld` ends past them.
+// Where a wave's stream reads: the expert's weight and (scale, bias) tables
+// as buffers, the lane's byte offsets at step 0 (its column's row; plus its
+// chunk g for weights, and its group for QS = 1), the bytes between the
+// wave's consecutive slabs and per unit.
+struct GxSrc {
+  __amdgpu_buffer_rsrc_t wr, sr, br;
+  uint32_t wl, sl;
+  uint32_t wslab, sslab;
+  uint32_t wunit, sunit;
+  uint32_t wlast, slast;  // uniform offsets of the last step's weights and (scale, bias) load
+  __device__ __forceinline__ uint32_t woff(const GxPos& p) const { return p.j * wslab + p.u * wunit; }
+  __device__ __forceinline__ uint32_t soff(const GxPos& p) const { return p.j * sslab + p.u * sunit; }
+};
+
+// The ring's first steps: weights of steps 0 .. GX_PF-1, (scale, bias) words
+// of steps 0 .. GX_UNROLL-1.  On return `wpos` / `spos` are the positions of
+// the next steps to load.  Every ring load is issued unconditionally (a step
+// past the wave's last re-reads the last one), so the compiler counts the
+// loads in flight exactly and never waits for more of them than it needs.
 template <int BITS, int QS, int GSQ>
-__device__ __forceinline__ void gx_fill(GxCursor<BITS>& ld, GxStep<BITS> (&ring)[GX_PF],
-                                        GxSb (&sbq)[GX_PF / QS], int units, int my_slabs, size_t wstride,
-                                        size_t gstride, int n, int chunks, int g, int gs_shift) {
+__device__ __forceinline__ void gx_fill(const GxSrc& src, GxRing<BITS, QS, GSQ>& ring, int T, int units,
+                                        GxPos& wpos, GxPos& spos) {
+  wpos = GxPos{0, 0};
+  spos = GxPos{0, 0};
 #pragma unroll
   for (int p = 0; p < GX_PF; ++p) {
-    gx_load<BITS, QS>(ld, ring[p], chunks, g, gs_shift);
-    if constexpr (QS > 1)
-      if (p % QS == 0) gx_load_sb<BITS, QS, GSQ>(ld, sbq[p / QS]);
-    ld.next(units, my_slabs, wstride, gstride, n);
+    gx_wload<BITS>(src.wr, src.wl, p < T ? src.woff(wpos) : src.wlast, ring.w[p]);
+    wpos.step(units);
   }
+#pragma unroll
+  for (int q = 0; q < GxRing<BITS, QS, GSQ>::kSb; ++q) {
+    gx_sbload<QS, GSQ>(src.sr, src.br, src.sl, q * QS < T ? src.soff(spos) : src.slast, ring.s[q], ring.b[q]);
+    spos.skip(QS, units);
+  }
+}
+
+// Whether the single-FMA dequantization is exact for the (scale, bias)
+// words of one load, per lane: lane group g checks word g % W of its
+// column's words with the packed check (the lane groups of a column hold the
+// same words); QS = 1: each lane its own group.  Sufficient, not necessary:
+// steps it does not clear are dequantized with fmaf, the same bits.
+template <typename TT, int QS, int W>
+__device__ __forceinline__ void gx_fast_add(FastQuick& fq, const uint32_t (&s)[W], const uint32_t (&b)[W], int g) {
+  // Words picked by masks, not by index: an array indexed by a lane value
+  // would be kept in scratch memory.
+  uint32_t sw, bw;
+  if constexpr (QS == 1) {
+    sw = s[0] | (s[0] << 16);
+    bw = b[0] | (b[0] << 16);
+  } else {
+    const uint32_t m1 = 0u - (uint32_t)(g & 1);
+    sw = s[0] ^ ((s[0] ^ s[1]) & m1);
+    bw = b[0] ^ ((b[0] ^ b[1]) & m1);
+    if constexpr (W == 4) {
+      const uint32_t m2 = 0u - (uint32_t)((g >> 1) & 1);
+      const uint32_t s23 = s[2] ^ ((s[2] ^ s[3]) & m1), b23 = b[2] ^ ((b[2] ^ b[3]) & m1);
+      sw = sw ^ ((sw ^ s23) & m2);
+      bw = bw ^ ((bw ^ b23) & m2);
+    }
+  }
+  fast_quick_add<TT>(fq, sw, bw);
+}
+
+// What one step of a wave's stream needs besides the ring.
+struct GxCtx {
+  int T, units, my_slabs, g, mbl;
+  uint32_t sel;
+  uint32_t aoff[4];
+  const unsigned char* xs;
+  int col0, n;
+  __amdgpu_buffer_rsrc_t yr;
+};
+
+// GX_UNROLL steps t0 .. t0+GX_UNROLL-1 of the stream, straight-line code:
+// no branch but the uniform one around a slab's stores, so the compiler's
+// count of loads in flight stays exact.  Steps past the wave's last (the
+// rounding of T up to a whole group) re-read the last step's words, compute
+// on them and store nothing.  MBL of the MB 16-row blocks are multiplied:
+// the ones that hold rows of the pass (each block read costs LDS bandwidth).
+template <typename TT, int BITS, int MB, int MBL, bool FAST, int QS, int GSQ>
+__device__ __forceinline__ void gx_group(const GxSrc& src, GxRing<BITS, QS, GSQ>& ring, GxPos& wpos, GxPos& spos,
+                                         GxPos& cur, int t0, f32x4 (&acc)[MB], const int (&orow)[MB][4],
+                                         const GxCtx& cx) {
+#pragma unroll
+  for (int p = 0; p < GX_UNROLL; ++p) {
+    const int t = t0 + p;
+    constexpr int kSbSlots = GxRing<BITS, QS, GSQ>::kSb;
+    const int q = (p / QS) % kSbSlots, I = p % QS;
+    const float sf = gx_sbv<TT, QS, GSQ>(ring.s[q], I, cx.sel);
+    const float bf = gx_sbv<TT, QS, GSQ>(ring.b[q], I, cx.sel);
+    const float s16 = sf * 0.0625f;
+    const float c0 = FAST ? fmaf(-1024.f, sf, bf) : 0.f, c1 = FAST ? fmaf(-64.f, sf, bf) : 0.f;
+    uint32_t(&wcur)[BITS] = ring.w[p % GX_PF];
+    u32x4 bop[4];
+    bop[0] = dequant_slice<TT, BITS, FAST, 0>(wcur, sf, s16, bf, c0, c1);
+    bop[1] = dequant_slice<TT, BITS, FAST, 1>(wcur, sf, s16, bf, c0, c1);
+    bop[2] = dequant_slice<TT, BITS, FAST, 2>(wcur, sf, s16, bf, c0, c1);
+    bop[3] = dequant_slice<TT, BITS, FAST, 3>(wcur, sf, s16, bf, c0, c1);
+    // Refill: weights of step t + GX_PF into this slot; after a (scale,
+    // bias) slot's last step, its words of GX_UNROLL steps later.
+    gx_wload<BITS>(src.wr, src.wl, t + GX_PF < cx.T ? src.woff(wpos) : src.wlast, wcur);
+    wpos.step(cx.units);
+    if (I == QS - 1) {
+      gx_sbload<QS, GSQ>(src.sr, src.br, src.sl, t + 1 - QS + GX_UNROLL < cx.T ? src.soff(spos) : src.slast,
+                         ring.s[q], ring.b[q]);
+      spos.skip(QS, cx.units);
+    }
+    const uint32_t ub = (uint32_t)cur.u * (MB * 4096u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const unsigned char* xa = cx.xs + cx.aoff[i] + ub;
+#pragma unroll
+      for (int mb = 0; mb < MBL; ++mb) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(xa + mb * 4096);
+        acc[mb] = Mfma16<TT>::run(a, bop[i], acc[mb]);
+      }
+    }
+    if (cur.u == cx.units - 1) {  // slab done (uniform)
+      if (cur.j < cx.my_slabs) {
+        // Rows of the pass and columns inside n store; the others take an
+        // offset past the buffer, which drops the store.
+        const int col = cx.col0 + 16 * GX_WAVES * cur.j;
+#pragma unroll
+        for (int mb = 0; mb < MBL; ++mb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool ok = orow[mb][i] >= 0 && col < cx.n;
+            const uint32_t off = ok ? ((uint32_t)orow[mb][i] * (uint32_t)cx.n + (uint32_t)col) * 2u : 0x80000000u;
+            __builtin_amdgcn_raw_buffer_store_b16(TT::from_f32(acc[mb][i]), cx.yr, off, 0, 0);
+          }
+      }
+#pragma unroll
+      for (int mb = 0; mb < MBL; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    cur.step(cx.units);
+  }
+}
+
+// A run of groups with MBL 16-row blocks, each group dequantized the fast way
+// when its (scale, bias) loads allow it.
+template <typename TT, int BITS, int MB, int MBL, int QS, int GSQ>
+__device__ __forceinline__ void gx_groups(const GxSrc& src, GxRing<BITS, QS, GSQ>& ring, GxPos wpos, GxPos spos,
+                                          const int (&orow)[MB][4], const GxCtx& cx) {
+  f32x4 acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  GxPos cur{0, 0};
+  for (int t0 = 0; t0 < cx.T; t0 += GX_UNROLL) {
+    // One decision per group: every (scale, bias) load the group reads.
+    FastQuick fq;
+    fast_quick_init(fq);
+#pragma unroll
+    for (int q = 0; q < GxRing<BITS, QS, GSQ>::kSb; ++q) gx_fast_add<TT, QS>(fq, ring.s[q], ring.b[q], cx.g);
+    if (__builtin_amdgcn_ballot_w64(!fast_quick_ok<TT>(fq)) == 0ull)
+      gx_group<TT, BITS, MB, MBL, true, QS, GSQ>(src, ring, wpos, spos, cur, t0, acc, orow, cx);
+    else
+      gx_group<TT, BITS, MB, MBL, false, QS, GSQ>(src, ring, wpos, spos, cur, t0, acc, orow, cx);
+  }
+}
+
+// The pass's stream: the code for its number of 16-row blocks (only the
+// blocks that hold rows of the pass are read and multiplied).
+template <typename TT, int BITS, int MB, int QS, int GSQ>
+__device__ __forceinline__ void gx_stream(const GxSrc& src, GxRing<BITS, QS, GSQ>& ring, GxPos wpos, GxPos spos,
+                                          const int (&orow)[MB][4], const GxCtx& cx) {
+  if constexpr (MB >= 4)
+    if (cx.mbl >= 3) {
+      if (cx.mbl == 4) return gx_groups<TT, BITS, MB, 4, QS, GSQ>(src, ring, wpos, spos, orow, cx);
+      return gx_groups<TT, BITS, MB, 3, QS, GSQ>(src, ring, wpos, spos, orow, cx);
+    }
+  if constexpr (MB >= 2)
+    if (cx.mbl == 2) return gx_groups<TT, BITS, MB, 2, QS, GSQ>(src, ring, wpos, spos, orow, cx);
+  gx_groups<TT, BITS, MB, 1, QS, GSQ>(src, ring, wpos, spos, orow, cx);
 }
 
 // First index i of the ascending a[0, n) with a[i] >= key (n if none), by one
@@ -176,78 +352,10 @@ __device__ __forceinline__ int wave_lower_bound(const uint32_t* __restrict__ a, 
   return lo;
 }
 
-template <typename TT, int BITS, int MB, bool FAST, int QS, int GSQ>
-__device__ __forceinline__ void gx_stream(GxCursor<BITS> ld, GxCursor<BITS> cp, GxStep<BITS> (&ring)[GX_PF],
-                                          GxSb (&sbq)[GX_PF / QS], int T, int units, int my_slabs, size_t wstride,
-                                          size_t gstride, int n, int chunks, int gs_shift, int g, int nl,
-                                          const unsigned char* xs, int k, const GxShared& sh, int mbl,
-                                          uint16_t* __restrict__ y) {
-  const int TP = (T + GX_PF - 1) / GX_PF * GX_PF;
-  const uint32_t sel = gx_sb_sel<TT>(g);
-  f32x4 acc[MB];
+__device__ __forceinline__ int wave_isum(int v) {
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  GxSb curq;
-  for (int t0 = 0; t0 < TP; t0 += GX_PF) {
-#pragma unroll
-    for (int p = 0; p < GX_PF; ++p) {
-      const int t = t0 + p;
-      const GxStep<BITS> cur = ring[p];
-      if constexpr (QS > 1)
-        if (p % QS == 0) curq = sbq[p / QS];
-      gx_load<BITS, QS>(ld, ring[p], chunks, g, gs_shift);  // clamped past the end: no branch, no wait
-      if constexpr (QS > 1)
-        if (p % QS == 0) gx_load_sb<BITS, QS, GSQ>(ld, sbq[p / QS]);
-      ld.next(units, my_slabs, wstride, gstride, n);
-      const int c = 4 * cp.u + g;
-      const bool live = t < T && c < chunks && cp.col < n;
-      float sf = 0.f, bf = 0.f;
-      if constexpr (QS == 1) {
-        sf = TT::to_f32((uint16_t)cur.s);
-        bf = TT::to_f32((uint16_t)cur.b);
-      } else {
-        sf = gx_sb_f32<TT, GSQ>(curq.s, p % QS, sel);
-        bf = gx_sb_f32<TT, GSQ>(curq.b, p % QS, sel);
-      }
-      sf = live ? sf : 0.f;
-      bf = live ? bf : 0.f;
-      const float s16 = sf * 0.0625f;
-      const float c0 = FAST ? fmaf(-1024.f, sf, bf) : 0.f, c1 = FAST ? fmaf(-64.f, sf, bf) : 0.f;
-      u32x4 bop[4];
-      bop[0] = dequant_slice<TT, BITS, FAST, 0>(cur.w, sf, s16, bf, c0, c1);
-      bop[1] = dequant_slice<TT, BITS, FAST, 1>(cur.w, sf, s16, bf, c0, c1);
-      bop[2] = dequant_slice<TT, BITS, FAST, 2>(cur.w, sf, s16, bf, c0, c1);
-      bop[3] = dequant_slice<TT, BITS, FAST, 3>(cur.w, sf, s16, bf, c0, c1);
-      const int cq = min(c, chunks - 1) * 4;  // first 16-byte chunk of this lane's 32 k
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        if (mb >= mbl) break;  // 16-row blocks past the pass's rows (wave-uniform)
-        const unsigned char* xr = xs + (size_t)(16 * mb + nl) * k * 2;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const u32x4 a = *reinterpret_cast<const u32x4*>(xr + (size_t)(((cq + i) ^ nl) * 16));
-          acc[mb] = Mfma16<TT>::run(a, bop[i], acc[mb]);
-        }
-      }
-      if (cp.u == units - 1) {  // slab done (uniform)
-        if (t < T && cp.col < n) {
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb) {
-            if (mb >= mbl) break;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int rl = 16 * mb + 4 * g + i;
-              const int r = sh.rows[rl];
-              if (r >= 0 && sh.xrow[rl] >= 0) y[(size_t)r * n + cp.col] = TT::from_f32(acc[mb][i]);
-            }
-          }
-        }
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-      cp.next(units, my_slabs, wstride, gstride, n);
-    }
-  }
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
 }
 
 template <typename TT, int BITS, int MB, int QS, int GSQ>
@@ -255,8 +363,9 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, const uint16_t* __restrict__ x, int x_rows,
     const uint32_t* __restrict__ lhs, const uint32_t* __restrict__ rhs, int n_rows,
-    uint16_t* __restrict__ y, int n, int k, int gs_shift, int sorted, int nc, int sb_vec,
+    uint16_t* __restrict__ y, int n, int k, int gs_shift, int sorted, int nc,
     unsigned int* __restrict__ status) {
+  static_assert(BITS == 4 || BITS == 8, "4- and 8-bit");
   constexpr int R = 16 * MB;
   __shared__ GxShared sh;
   extern __shared__ __attribute__((aligned(16))) unsigned char xs[];  // R x K activations
@@ -267,10 +376,9 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
   const int c0 = blockIdx.x * nc;
   const int ncols = min(nc, n - c0);
   const int chunks = k >> 5;
-  const int units = (chunks + 3) >> 2;
+  const int units = chunks >> 2;  // k % 128 == 0
   const int G = k >> gs_shift;
-  const size_t words_per_row = (size_t)k * BITS / 32;
-  const uint32_t* we = w + (size_t)e * n * words_per_row;
+  const uint32_t row_bytes = (uint32_t)k * BITS / 8, grow_bytes = (uint32_t)G * 2u;
   const uint16_t* se = scales + (size_t)e * n * G;
   const uint16_t* be = biases + (size_t)e * n * G;
 
@@ -304,19 +412,80 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
     }
   };
 
-  // 1. Rows routed to e.
+  // 1. Where this wave's weight stream reads (16-column slabs wave,
+  //    wave + 8, ... of the chunk).
+  const int nslab = (ncols + 15) >> 4;
+  const int my_slabs = nslab > wave ? (nslab - wave + GX_WAVES - 1) / GX_WAVES : 0;
+  const int T = my_slabs * units;  // steps of this wave
+  GxSrc src;
+  src.wr = __builtin_amdgcn_make_buffer_rsrc((void*)(w + (size_t)e * n * (row_bytes / 4)), 0,
+                                             (int)((uint32_t)n * row_bytes), 0x00020000);
+  src.sr = __builtin_amdgcn_make_buffer_rsrc((void*)se, 0, (int)((uint32_t)n * grow_bytes), 0x00020000);
+  src.br = __builtin_amdgcn_make_buffer_rsrc((void*)be, 0, (int)((uint32_t)n * grow_bytes), 0x00020000);
+  const int col0 = c0 + 16 * wave + nl;  // columns past n read past the buffers: zeros, never stored
+  src.wl = (uint32_t)col0 * row_bytes + (uint32_t)g * (4u * BITS);
+  src.sl = (uint32_t)col0 * grow_bytes + (QS == 1 ? (((uint32_t)g * 32u) >> gs_shift) * 2u : 0u);
+  src.wslab = 16u * GX_WAVES * row_bytes;
+  src.sslab = 16u * GX_WAVES * grow_bytes;
+  src.wunit = 16u * BITS;               // 4 chunks of 4 * BITS bytes
+  src.sunit = (256u >> gs_shift);       // 128 / gs groups of 2 bytes
+  {
+    const int tl = T > 0 ? T - 1 : 0;     // the last step (a wave without slabs re-reads step 0)
+    const GxPos last{tl % units, tl / units};
+    const GxPos lastq{last.u / QS * QS, last.j};
+    src.wlast = src.woff(last);
+    src.slast = src.soff(lastq);
+  }
+  GxRing<BITS, QS, GSQ> ring;
+  GxPos wpos, spos;
+
+  // 2. Rows routed to e, on a memory system not yet busy with this
+  //    workgroup's weights (the routing, the activation rows and their
+  //    loads are three dependent round trips).
   const int nblk = (n_rows + 63) >> 6;
   if (sorted) {
-    // [lo, hi) = equal range of e in the ascending rhs; waves 0 and 1 search
-    // its two ends at once.
-    if (wave < 2) {
-      const int b = wave_lower_bound(rhs, n_rows, e + (uint32_t)wave, lane);
-      if (lane == 0) sh.cnt[wave] = b;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      sh.lo = sh.cnt[0];
-      sh.total = sh.cnt[1] - sh.cnt[0];
+    if (n_rows <= GX_COUNT_ROWS) {
+      // [lo, lo + total): rows below e and rows at e of the ascending rhs,
+      // counted over every row in one round of loads.
+      uint32_t v[GX_COUNT_ROWS / GX_THREADS];
+#pragma unroll
+      for (int j = 0; j < GX_COUNT_ROWS / GX_THREADS; ++j) {
+        const int r = tid + j * GX_THREADS;
+        v[j] = r < n_rows ? rhs[r] : 0xffffffffu;
+      }
+      int lt = 0, le = 0;
+#pragma unroll
+      for (int j = 0; j < GX_COUNT_ROWS / GX_THREADS; ++j) {
+        lt += v[j] < e ? 1 : 0;
+        le += v[j] <= e ? 1 : 0;
+      }
+      lt = wave_isum(lt);
+      le = wave_isum(le);
+      if (lane == 0) {
+        sh.cnt[2 * wave] = lt;
+        sh.cnt[2 * wave + 1] = le;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        int a = 0, b = 0;
+        for (int i = 0; i < GX_WAVES; ++i) {
+          a += sh.cnt[2 * i];
+          b += sh.cnt[2 * i + 1];
+        }
+        sh.lo = a;
+        sh.total = b - a;
+      }
+    } else {
+      // Equal range of e by two wave-parallel searches at once.
+      if (wave < 2) {
+        const int b = wave_lower_bound(rhs, n_rows, e + (uint32_t)wave, lane);
+        if (lane == 0) sh.cnt[wave] = b;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        sh.lo = sh.cnt[0];
+        sh.total = sh.cnt[1] - sh.cnt[0];
+      }
     }
   } else {
     for (int b = wave; b < nblk; b += GX_WAVES) {
@@ -326,16 +495,17 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
     }
     __syncthreads();
     if (tid == 0) {  // exclusive prefix over the blocks
-      int run = 0;
+      int run_ = 0;
       for (int b = 0; b < nblk; ++b) {
         const int c = sh.cnt[b];
-        sh.cnt[b] = run;
-        run += c;
+        sh.cnt[b] = run_;
+        run_ += c;
       }
-      sh.total = run;
+      sh.total = run_;
       sh.lo = 0;
     }
   }
+
   __syncthreads();
   const int total = sh.total;
   if (total == 0) {  // uniform
@@ -343,68 +513,21 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
     return;
   }
 
-  // Wave w's slabs: 16-column slabs w, w+8, ... of the chunk.  Their first
-  // GX_PF weight steps are requested now, so the stream is in flight while
-  // the constants are voted on and the activations staged.
-  const int nslab = (ncols + 15) >> 4;
-  const int my_slabs = nslab > wave ? (nslab - wave + GX_WAVES - 1) / GX_WAVES : 0;
-  const int T = my_slabs * units;  // live steps of this wave
-  const size_t wstride = (size_t)16 * GX_WAVES * words_per_row, gstride = (size_t)16 * GX_WAVES * G;
-  GxCursor<BITS> start;
-  start.u = 0;
-  start.slab = 0;
-  start.col = c0 + 16 * wave + nl;
-  const int col0 = min(start.col, n - 1);
-  start.wrow = we + (size_t)col0 * words_per_row;
-  start.srow = se + (size_t)col0 * G;
-  start.brow = be + (size_t)col0 * G;
-  GxStep<BITS> ring[GX_PF];
-  GxSb sbq[GX_PF / QS];
-  GxCursor<BITS> ld = start;
-  if (T > 0) gx_fill<BITS, QS, GSQ>(ld, ring, sbq, units, my_slabs, wstride, gstride, n, chunks, g, gs_shift);
-
-  // 2. Fast-path vote over the chunk's (column, group) pairs.  The chunk's
-  //    columns are consecutive rows of the expert's [n, G] tables, so its
-  //    pairs are one contiguous run of ncols * G entries: 16-byte segments
-  //    (when the run starts 16-byte aligned) get the packed exponent check,
-  //    and the exact predicate where that one does not clear a thread's
-  //    segments; the tail and unaligned runs go pair by pair.
-  bool ok = true;
-  const size_t run0 = (size_t)c0 * G;
-  const int run = ncols * G;
-  const int nvec = sb_vec ? run >> 3 : 0;
-  for (int i0 = tid; i0 < nvec; i0 += 4 * GX_THREADS) {
-    u32x4 sv[4], bv[4];
-    bool live[4];
+  // LDS offsets of this lane's A pieces: 16-byte piece i of chunk 4u + g of
+  // row nl of a block is slot (4g + i) ^ nl of the row (unit u, block mb at
+  // (u * MB + mb) * 4096 bytes).
+  GxCtx cx;
+  cx.T = T;
+  cx.units = units;
+  cx.my_slabs = my_slabs;
+  cx.g = g;
+  cx.sel = gx_sb_sel<TT>(g);
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      const int i = i0 + h * GX_THREADS;
-      live[h] = i < nvec;
-      if (live[h]) {
-        sv[h] = *reinterpret_cast<const u32x4*>(se + run0 + (size_t)i * 8);
-        bv[h] = *reinterpret_cast<const u32x4*>(be + run0 + (size_t)i * 8);
-      } else {  // a pair the packed check accepts
-        sv[h] = bv[h] = u32x4{0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};
-      }
-    }
-    FastQuick fq;
-    fast_quick_init(fq);
-#pragma unroll
-    for (int h = 0; h < 4; ++h)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) fast_quick_add<TT>(fq, sv[h][q], bv[h][q]);
-    if (!fast_quick_ok<TT>(fq)) {
-#pragma unroll
-      for (int h = 0; h < 4; ++h)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          ok &= !live[h] | (fast_ok_bits<TT>(sv[h][q] & 0xffffu, bv[h][q] & 0xffffu) &
-                            fast_ok_bits<TT>(sv[h][q] >> 16, bv[h][q] >> 16));
-    }
-  }
-  for (int i = 8 * nvec + tid; i < run; i += GX_THREADS) ok &= fast_ok_bits<TT>(se[run0 + i], be[run0 + i]);
-  bool fast = __syncthreads_and(ok);
-  if constexpr (BITS != 4 && BITS != 8) fast = false;
+  for (int i = 0; i < 4; ++i) cx.aoff[i] = (uint32_t)nl * 256u + (uint32_t)(((4 * g + i) ^ nl) * 16);
+  cx.xs = xs;
+  cx.col0 = col0;
+  cx.n = n;
+  cx.yr = __builtin_amdgcn_make_buffer_rsrc((void*)y, 0, (int)((uint32_t)n_rows * (uint32_t)n * 2u), 0x00020000);
 
   for (int p0 = 0; p0 < total; p0 += R) {
     // 3. The pass's rows and activation rows.
@@ -436,52 +559,67 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
     }
     __syncthreads();
 
-    // 4. Activation rows into LDS in the dequantizer's slot order, 16-byte
-    //    chunk q of row i at i*K*2 + (q ^ (i & 15))*16.  Only the pass's
-    //    rows are staged, 8 loads per thread in flight: the other rows of
-    //    its 16-row blocks keep stale LDS bytes, which reach only their own
-    //    output rows (MFMA rows are independent), and those are not stored.
-    const int kq = k >> 3;  // 16-byte chunks per row
-    const int nst = min(R, total - p0) * kq;
-    for (int idx = tid; idx < nst; idx += GX_THREADS * 8) {
-      u32x4 v[8];
+    // 4. Activation rows into LDS in the dequantizer's slot order: every
+    //    16-byte item of the pass (at most GX_XITEMS per thread) requested at
+    //    once, then the first weight steps (so the activations do not queue
+    //    behind them), then the LDS writes.  Only the pass's rows are
+    //    staged: the other rows of its 16-row blocks keep stale LDS bytes,
+    //    which reach only their own output rows (MFMA rows are independent),
+    //    and those are not stored.
+    const int kq = k >> 3;  // 16-byte items per row
+    const int nst = min(R, total - p0) * kq;  // <= R * K / 8 <= GX_XITEMS * GX_THREADS
+    {
+      // Item id = tid + h * GX_THREADS is row id / kq, 16-byte piece id % kq;
+      // both advance by fixed amounts per h (one division, not one per item).
+      const int di = GX_THREADS / kq, dq = GX_THREADS - di * kq;
+      int ii[GX_XITEMS], qq[GX_XITEMS];
+      ii[0] = tid / kq;
+      qq[0] = tid - ii[0] * kq;
 #pragma unroll
-      for (int h = 0; h < 8; ++h) {
-        const int id = idx + h * GX_THREADS;
+      for (int h = 1; h < GX_XITEMS; ++h) {
+        const int q1 = qq[h - 1] + dq;
+        const bool wrap = q1 >= kq;
+        qq[h] = wrap ? q1 - kq : q1;
+        ii[h] = ii[h - 1] + di + (wrap ? 1 : 0);
+      }
+      u32x4 v[GX_XITEMS];
+#pragma unroll
+      for (int h = 0; h < GX_XITEMS; ++h) {
+        const int id = tid + h * GX_THREADS;
         v[h] = u32x4{0u, 0u, 0u, 0u};
         if (id < nst) {
-          const int i = id / kq, q = id - i * kq;
-          const int xi = sh.xrow[i];
-          if (xi >= 0) v[h] = *reinterpret_cast<const u32x4*>(x + (size_t)xi * k + (size_t)q * 8);
+          const int xi = sh.xrow[ii[h]];
+          if (xi >= 0) v[h] = *reinterpret_cast<const u32x4*>(x + (size_t)xi * k + (size_t)qq[h] * 8);
         }
       }
+      gx_fill<BITS, QS, GSQ>(src, ring, T, units, wpos, spos);
 #pragma unroll
-      for (int h = 0; h < 8; ++h) {
-        const int id = idx + h * GX_THREADS;
+      for (int h = 0; h < GX_XITEMS; ++h) {
+        const int id = tid + h * GX_THREADS;
         if (id < nst) {
-          const int i = id / kq, q = id - i * kq;
-          *reinterpret_cast<u32x4*>(xs + (size_t)i * k * 2 + (size_t)((q ^ (i & 15)) * 16)) =
-              interleave_x<BITS>(v[h]);
+          const int i = ii[h], q = qq[h];
+          const int r16 = i & 15;
+          const uint32_t off = (uint32_t)((q >> 4) * MB + (i >> 4)) * 4096u + (uint32_t)r16 * 256u +
+                               (uint32_t)(((q & 15) ^ r16) * 16);
+          *reinterpret_cast<u32x4*>(xs + off) = interleave_x<BITS>(v[h]);
         }
       }
     }
+    // This lane's output rows: row 16 mb + 4 g + i of the pass (-1: none).
+    int orow[MB][4];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rl = 16 * mb + 4 * g + i;
+        orow[mb][i] = sh.rows[rl] >= 0 && sh.xrow[rl] >= 0 ? sh.rows[rl] : -1;
+      }
     __syncthreads();
 
-    // 5. Stream the weights of this wave's slabs; only the 16-row blocks
-    //    that hold rows of this pass are multiplied.
-    const int mbl = (min(R, total - p0) + 15) >> 4;
-    if (T > 0) {
-      if (p0 > 0) {  // a further pass streams the weights again
-        ld = start;
-        gx_fill<BITS, QS, GSQ>(ld, ring, sbq, units, my_slabs, wstride, gstride, n, chunks, g, gs_shift);
-      }
-      if (fast)
-        gx_stream<TT, BITS, MB, true, QS, GSQ>(ld, start, ring, sbq, T, units, my_slabs, wstride, gstride, n, chunks, gs_shift,
-                                      g, nl, xs, k, sh, mbl, y);
-      else
-        gx_stream<TT, BITS, MB, false, QS, GSQ>(ld, start, ring, sbq, T, units, my_slabs, wstride, gstride, n, chunks,
-                                       gs_shift, g, nl, xs, k, sh, mbl, y);
-    }
+    // 5. Stream the weights of this wave's slabs (again for every further
+    //    pass).
+    cx.mbl = (min(R, total - p0) + 15) >> 4;
+    if (T > 0) gx_stream<TT, BITS, MB, QS, GSQ>(src, ring, wpos, spos, orow, cx);
     __syncthreads();  // LDS rows / activations are rewritten by the next pass
   }
   check_rows();
@@ -490,7 +628,7 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
 template <typename TT, int BITS, int MB, int QS, int GSQ>
 hipError_t launch_q(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
                     const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
-                    int gs_shift, int n_chunks, int nc, int sb_vec, unsigned int* status) {
+                    int gs_shift, int n_chunks, int nc, unsigned int* status) {
   static const hipError_t attr = [] {
     const void* fn = reinterpret_cast<const void*>(&gather_expert_kernel<TT, BITS, MB, QS, GSQ>);
     hipFuncAttributes fa;
@@ -504,7 +642,7 @@ hipError_t launch_q(hipStream_t s, const QuantArgs& q, const void* x, int x_rows
   hipLaunchKernelGGL((gather_expert_kernel<TT, BITS, MB, QS, GSQ>), dim3((unsigned)n_chunks, (unsigned)n_experts),
                      dim3(GX_THREADS), lds, s, q.w, static_cast<const uint16_t*>(q.scales),
                      static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x), x_rows, lhs,
-                     rhs, n_rows, static_cast<uint16_t*>(y), n, k, gs_shift, (int)sorted, nc, sb_vec, status);
+                     rhs, n_rows, static_cast<uint16_t*>(y), n, k, gs_shift, (int)sorted, nc, status);
   return hipGetLastError();
 }
 
@@ -518,16 +656,20 @@ hipError_t launch_mb(hipStream_t s, const QuantArgs& q, const void* x, int x_row
                      int gs_shift, int n_chunks, int nc, unsigned int* status) {
   const int G = k / q.gs, units = k / 128;
   const uintptr_t al = reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases);
-  // Vote runs start at (e n + c0) G entries, c0 a multiple of 128.
-  const int sb_vec = ((long)n * G % 8 == 0) && (al % 16 == 0);
+  // Buffer offsets of one expert's tables and of Y stay inside 31 bits.
+  if ((uint64_t)n * k * BITS / 8 >= (1ull << 31) || (uint64_t)n * G * 2 >= (1ull << 31) ||
+      (uint64_t)n_rows * n * 2 >= (1ull << 31))
+    return hipErrorInvalidValue;
   static const int forced = env_int("CPQ_GATHER_QS", 0);
 #define CPQ_GXQ(QS, GSQ)                                                                                  \
   return launch_q<TT, BITS, MB, QS, GSQ>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted,   \
-                                         gs_shift, n_chunks, nc, sb_vec, status)
+                                         gs_shift, n_chunks, nc, status)
+  // Each expert's tables start (n G entries apart) aligned to the vector too.
+  const long eb = (long)n * G * 2;
   if (forced != 1) {
-    if (q.gs == 64 && units % 4 == 0 && al % 16 == 0 && forced != 2) CPQ_GXQ(4, 64);
-    if (q.gs == 64 && units % 2 == 0 && al % 8 == 0) CPQ_GXQ(2, 64);
-    if (q.gs == 128 && units % 4 == 0 && al % 8 == 0) CPQ_GXQ(4, 128);
+    if (q.gs == 64 && units % 4 == 0 && al % 16 == 0 && eb % 16 == 0 && forced != 2) CPQ_GXQ(4, 64);
+    if (q.gs == 64 && units % 2 == 0 && al % 8 == 0 && eb % 8 == 0) CPQ_GXQ(2, 64);
+    if (q.gs == 128 && units % 4 == 0 && al % 8 == 0 && eb % 8 == 0) CPQ_GXQ(4, 128);
   }
   CPQ_GXQ(1, 64);
 #undef CPQ_GXQ
@@ -566,10 +708,12 @@ hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, int x_rows
 
 }  // namespace
 
-bool gather_expert_supported(int bits, int n_rows, int k) {
-  // k % 128: whole 16-chunk swizzle groups per staged row.
+bool gather_expert_supported(int bits, int n_rows, int n, int k) {
+  // k % 128: whole units per staged row; one expert's weights and Y within
+  // the 31-bit buffer offsets.
   return (bits == 4 || bits == 8) && k % 128 == 0 && n_rows <= 64 * GX_MAXBLK &&
-         (size_t)16 * k * 2 <= (size_t)GX_XBYTES;
+         (size_t)16 * k * 2 <= (size_t)GX_XBYTES && (uint64_t)n * k * bits / 8 < (1ull << 31) &&
+         (uint64_t)n_rows * n * 2 < (1ull << 31);
 }
 
 hipError_t launch_gather_expert(hipStream_t s, const QuantArgs& q, const void* x, int x_rows,

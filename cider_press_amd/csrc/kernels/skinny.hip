@@ -519,7 +519,7 @@ hipError_t launch_gather_t(hipStream_t s, const QuantArgs& q, const void* x, int
                            int n_experts, int n, int k, bool sorted, unsigned int* status) {
   if (n_rows == 0) return hipSuccess;
   const int gs_shift = shift_of(q.gs);
-  if (gather_expert_supported(BITS, n_rows, k)) {  // validates the indices itself
+  if (gather_expert_supported(BITS, n_rows, n, k)) {  // validates the indices itself
     static const int cus = [] {
       int dev = 0, cu = 0;
       if (hipGetDevice(&dev) != hipSuccess ||
@@ -574,8 +574,8 @@ bool skinny_fits(int k, int gs) {
   return gs > 0 && slab_consts_bytes(k, gs) + sizeof(TileShared<8, kMaxMB>) <= (size_t)160 * 1024;
 }
 
-bool gather_supported(int bits, int n_rows, int k, int gs) {
-  return gather_expert_supported(bits, n_rows, k) ||
+bool gather_supported(int bits, int n_rows, int n, int k, int gs) {
+  return gather_expert_supported(bits, n_rows, n, k) ||
          (gs > 0 && slab_consts_bytes(k, gs) + sizeof(TileShared<4, kMaxMB>) <= (size_t)160 * 1024);
 }
 

@@ -784,7 +784,7 @@ cpq_status cpq_affine_gather_qmm(cpq_commands* cmds, cpq_dtype dtype, const void
   if (st != CPQ_OK) return st;
   if (x_rows == 0)
     return fail(CPQ_ERR_INVALID_ARGUMENT, "affine_gather_qmm: x has no rows but lhs_indices select some");
-  if (!cpq::gather_supported((int)bits, (int)n_rows, (int)k, (int)group_size))
+  if (!cpq::gather_supported((int)bits, (int)n_rows, (int)n, (int)k, (int)group_size))
     return fail(CPQ_ERR_INVALID_ARGUMENT,
                 "affine_gather_qmm: K=" + std::to_string(k) + " at group_size " + std::to_string(group_size) +
                     " has " + std::to_string(k / group_size) +
