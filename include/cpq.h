@@ -326,8 +326,10 @@ cpq_status cpq_check_gather_args(cpq_dtype dtype, size_t x_rows, size_t w_q_len,
  * for w_q, T elements otherwise; stride 0 broadcasts), and writes its
  * [M, N] (qmv: [N]) block of y contiguously at z*M*N.  Each element's matrix
  * must lie inside its buffer; w_q strides must be multiples of 4 words and x
- * strides of 8 elements.  Each element is one single-matrix launch on the
- * session stream (encode only). */
+ * strides of 8 elements.  Encode only: weights shared by every element with
+ * dense activations run as one matmul over all rows; otherwise the decode
+ * kernels take the batch in a grid dimension where the shape allows, else
+ * each element is one single-matrix launch on the session stream. */
 cpq_status cpq_affine_qmm_t_batched(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q, size_t w_q_len,
                                     const void* scales, size_t scales_len, const void* biases,
                                     size_t biases_len, const void* x, size_t x_len, void* y, size_t y_len,
