@@ -567,14 +567,18 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
     //    which reach only their own output rows (MFMA rows are independent),
     //    and those are not stored.
     const int kq = k >> 3;  // 16-byte items per row
-    const int nst = min(R, total - p0) * kq;  // <= R * K / 8 <= GX_XITEMS * GX_THREADS
-    {
-      // Item id = tid + h * GX_THREADS is row id / kq, 16-byte piece id % kq;
+    const int nst = min(R, total - p0) * kq;  // <= R * K / 8
+    // Rounds of GX_XITEMS items per thread (one round when that covers
+    // R * K / 8); the bound is uniform, and nst > 0, so every thread runs the
+    // first round and issues the weight steps in it.
+    for (int base = 0; base < nst; base += GX_XITEMS * GX_THREADS) {
+      const int id0 = base + tid;
+      // Item id = id0 + h * GX_THREADS is row id / kq, 16-byte piece id % kq;
       // both advance by fixed amounts per h (one division, not one per item).
       const int di = GX_THREADS / kq, dq = GX_THREADS - di * kq;
       int ii[GX_XITEMS], qq[GX_XITEMS];
-      ii[0] = tid / kq;
-      qq[0] = tid - ii[0] * kq;
+      ii[0] = id0 / kq;
+      qq[0] = id0 - ii[0] * kq;
 #pragma unroll
       for (int h = 1; h < GX_XITEMS; ++h) {
         const int q1 = qq[h - 1] + dq;
@@ -585,17 +589,17 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
       u32x4 v[GX_XITEMS];
 #pragma unroll
       for (int h = 0; h < GX_XITEMS; ++h) {
-        const int id = tid + h * GX_THREADS;
+        const int id = id0 + h * GX_THREADS;
         v[h] = u32x4{0u, 0u, 0u, 0u};
         if (id < nst) {
           const int xi = sh.xrow[ii[h]];
           if (xi >= 0) v[h] = *reinterpret_cast<const u32x4*>(x + (size_t)xi * k + (size_t)qq[h] * 8);
         }
       }
-      gx_fill<BITS, QS, GSQ>(src, ring, T, units, wpos, spos);
+      if (base == 0) gx_fill<BITS, QS, GSQ>(src, ring, T, units, wpos, spos);
 #pragma unroll
       for (int h = 0; h < GX_XITEMS; ++h) {
-        const int id = tid + h * GX_THREADS;
+        const int id = id0 + h * GX_THREADS;
         if (id < nst) {
           const int i = ii[h], q = qq[h];
           const int r16 = i & 15;
