@@ -594,6 +594,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // 7. Store: res[r] is block (row block 2r + kq/2, column block kq%2) of N
   //    half nh: element e at row 32 rb + 8(e/4) + 4h + e%4, column l32.
   const int gcol = col0 + 64 * nh + 32 * (kq & 1) + l32;
+  if (row0 + DBM <= m && col0 + DBN <= n) {
+    // A whole tile inside Y: the lane's column and row half in the per-lane
+    // offset, each element's row in the scalar one (no per-store address
+    // arithmetic or checks).
+    const __amdgpu_buffer_rsrc_t yr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)y, 0, (int)((uint32_t)m * (uint32_t)n * 2u), 0x00020000);
+    const uint32_t lane_off = ((uint32_t)(row0 + 4 * h) * (uint32_t)n + (uint32_t)gcol) * 2u;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int rb = 2 * r + (kq >> 1);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t row_off = (uint32_t)(32 * rb + 8 * (e >> 2) + (e & 3)) * (uint32_t)n * 2u;
+        __builtin_amdgcn_raw_buffer_store_b16(TT::from_f32(res[r][e]), yr, lane_off, row_off, 0);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const int rb = 2 * r + (kq >> 1);
@@ -619,8 +637,8 @@ bool qmm_dma_fits(int m, int n, int k, int gs, int bits, int split) {
   if (dma_lds(k, gs, split) > (size_t)DLDS_MAX) return false;
   const uint64_t tiles = (uint64_t)((m + DBM - 1) / DBM) * ((n + DBN - 1) / DBN);
   if (split > 1 && (tiles > (uint64_t)kDmaReadyOffset || tiles * split > (uint64_t)kDmaMaxParts)) return false;
-  const uint64_t xb = (uint64_t)m * k * 2, wb = (uint64_t)(n + DBN) * k / 2;
-  return xb < (1ull << 31) && wb < (1ull << 31);
+  const uint64_t xb = (uint64_t)m * k * 2, wb = (uint64_t)(n + DBN) * k / 2, yb = (uint64_t)m * n * 2;
+  return xb < (1ull << 31) && wb < (1ull << 31) && yb < (1ull << 31);
 }
 
 int qmm_dma_split(int m, int n, int k, int gs, int bits, int cu_count) {
