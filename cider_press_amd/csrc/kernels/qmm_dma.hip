@@ -46,6 +46,8 @@
 // 4(m/8) + m%4.
 #include <algorithm>
 
+#include <type_traits>
+
 #include "../cpq_internal.hpp"
 #include "common.hpp"
 
@@ -471,35 +473,52 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __syncthreads();  // every wave done with the rings (all copies landed: the last stage waited for them)
   float* ep = reinterpret_cast<float*>(smem);
   f32x16 res[2];
+  // Specialised by the wave's K quarter: a wave parks only the three blocks
+  // other waves add (its own block, slot kq, stays in registers) and reads
+  // the other three quarters' slot kq; the sums keep K-quarter order.
+  auto reduce = [&](auto KQ) {
+    constexpr int KQC = decltype(KQ)::value;
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    float* mine = ep + (wave * 64 + lane) * DEPI;
+    for (int r = 0; r < 2; ++r) {
+      float* mine = ep + (wave * 64 + lane) * DEPI;
 #pragma unroll
-    for (int ii = 0; ii < 2; ++ii)
+      for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-      for (int cb = 0; cb < 2; ++cb)
+        for (int cb = 0; cb < 2; ++cb) {
+          if (ii * 2 + cb == KQC) continue;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<f32x4*>(mine + (ii * 2 + cb) * 16 + 4 * q) =
+                f32x4{acc[2 * r + ii][cb][4 * q], acc[2 * r + ii][cb][4 * q + 1], acc[2 * r + ii][cb][4 * q + 2],
+                      acc[2 * r + ii][cb][4 * q + 3]};
+        }
+      __syncthreads();
+      // All 12 reads first, then the sums in K-quarter order.
+      f32x4 pk[4][4];
+#pragma unroll
+      for (int k2 = 0; k2 < 4; ++k2)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          *reinterpret_cast<f32x4*>(mine + (ii * 2 + cb) * 16 + 4 * q) =
-              f32x4{acc[2 * r + ii][cb][4 * q], acc[2 * r + ii][cb][4 * q + 1], acc[2 * r + ii][cb][4 * q + 2],
-                    acc[2 * r + ii][cb][4 * q + 3]};
-    __syncthreads();
-    // All 16 reads first, then the sums in K-quarter order.
-    f32x4 pk[4][4];
+          pk[k2][q] = k2 == KQC
+                          ? f32x4{acc[2 * r + KQC / 2][KQC % 2][4 * q], acc[2 * r + KQC / 2][KQC % 2][4 * q + 1],
+                                  acc[2 * r + KQC / 2][KQC % 2][4 * q + 2], acc[2 * r + KQC / 2][KQC % 2][4 * q + 3]}
+                          : *reinterpret_cast<const f32x4*>(ep + ((4 * nh + k2) * 64 + lane) * DEPI + 16 * KQC + 4 * q);
 #pragma unroll
-    for (int k2 = 0; k2 < 4; ++k2)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        pk[k2][q] = *reinterpret_cast<const f32x4*>(ep + ((4 * nh + k2) * 64 + lane) * DEPI + 16 * kq + 4 * q);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f32x4 sum = ((pk[0][q] + pk[1][q]) + pk[2][q]) + pk[3][q];
-      res[r][4 * q] = sum[0];
-      res[r][4 * q + 1] = sum[1];
-      res[r][4 * q + 2] = sum[2];
-      res[r][4 * q + 3] = sum[3];
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 sum = ((pk[0][q] + pk[1][q]) + pk[2][q]) + pk[3][q];
+        res[r][4 * q] = sum[0];
+        res[r][4 * q + 1] = sum[1];
+        res[r][4 * q + 2] = sum[2];
+        res[r][4 * q + 3] = sum[3];
+      }
+      __syncthreads();
     }
-    __syncthreads();
+  };
+  switch (kq) {
+    case 0: reduce(std::integral_constant<int, 0>{}); break;
+    case 1: reduce(std::integral_constant<int, 1>{}); break;
+    case 2: reduce(std::integral_constant<int, 2>{}); break;
+    default: reduce(std::integral_constant<int, 3>{}); break;
   }
 
   // 6. Split K.  A workgroup parks its partial tile and counts its arrival
