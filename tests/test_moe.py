@@ -69,6 +69,9 @@ def _logits(rng, tokens, E, dtype):
     (33, 1000, 16, True, "f16"),
     (1, 8, 8, False, "bf16"),        # every expert picked
     (700, 60, 4, True, "bf16"),      # several sort blocks, E not a multiple of 64
+    (300, 4, 4, False, "bf16"),      # every row of a token on the 4 experts: long equal runs
+    (2100, 64, 8, True, "bf16"),     # 66 sort blocks
+    (1100, 1000, 2, True, "f16"),    # 9 sort blocks x 1000 experts
 ])
 def test_route_and_sort(device, tokens, E, k, normalize, dtype):
     rng = np.random.default_rng(tokens * 7 + E + k)
