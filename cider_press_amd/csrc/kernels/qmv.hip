@@ -774,14 +774,20 @@ hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, i
   const size_t G = (size_t)k / q.gs;
   const size_t lds = (size_t)k * 2 + 16 * (G + 1) * 16 + 8 * 16 * 4;
   if constexpr (BITS == 4 || BITS == 8) {
-    // Few row blocks (under two per CU): 8 waves per block keep two waves per SIMD.
-    static const int forced = env_int("CPQ_QMV_WAVES", 0);  // tuning hook: 4 or 8
-    const int waves = forced == 4 || forced == 8 ? (lean_fits<BITS>(q, n, k, forced) ? forced : 4)
-                      : (n + 15) / 16 < 512 && lean_fits<BITS>(q, n, k, 8) ? 8 : 4;
+    // Few row blocks (under two per CU): 8 waves per block keep two waves per
+    // SIMD; 12 (three per SIMD) where K splits into 12 ranges of at least 8
+    // steps (K = 12288: 9.2 -> 8.4 us at N = 4096).
+    static const int forced = env_int("CPQ_QMV_WAVES", 0);  // tuning hook: 4, 8 or 12
+    const bool few = (n + 15) / 16 < 512;
+    const int waves = forced == 4 || forced == 8 || forced == 12 ? (lean_fits<BITS>(q, n, k, forced) ? forced : 4)
+                      : few && lean_fits<BITS>(q, n, k, 12) && k / (128 * 12) >= 8 ? 12
+                      : few && lean_fits<BITS>(q, n, k, 8)                          ? 8
+                                                                                    : 4;
     if (lean_fits<BITS>(q, n, k, waves)) {
       const int sh = shift_of(q.gs);
       const size_t llds = (size_t)waves * lean_wave_lds(k / (128 * waves), sh) + (size_t)waves * 16 * 4;
       if (llds <= 160 * 1024 - 1024) {
+        if (waves == 12) return launch_lean_w<TT, BITS, 12>(s, q, x, y, n, k, llds);
         if (waves == 8) return launch_lean_w<TT, BITS, 8>(s, q, x, y, n, k, llds);
         return launch_lean_w<TT, BITS, 4>(s, q, x, y, n, k, llds);
       }
