@@ -67,12 +67,11 @@ constexpr int DEPI = 64 + 4;                    // epilogue floats per lane (pad
 constexpr int DEPI_BYTES = 8 * 64 * DEPI * 4;   // 139264
 constexpr int DLDS_MAX = 160 * 1024 - 256;      // dynamic LDS budget next to the vote words
 constexpr int DPART = DBM * DBN;                // floats per partial tile
-// Split-K words at the head of the scratch (64 KiB): per tile an arrival
-// counter at [t]; per (tile, k-part) a "part parked" word at
-// [kDmaReadyOffset + t*split + kk] (0, or how it was parked: 1 memory side,
-// 2 the XCD's L2) and the XCD id + 1 of the workgroup computing it at
+// Split-K words at the head of the scratch (64 KiB): per tile at [t] the
+// arrivals (low 8 bits) and, bit 8 + kk, k-part kk parked through its XCD's
+// L2; per (tile, k-part) the XCD id + 1 of the workgroup computing it at
 // [kDmaXccOffset + t*split + kk].  All are zero between launches.
-constexpr int kDmaReadyOffset = 4096;
+constexpr int kDmaMaxTiles = 4096;
 constexpr int kDmaXccOffset = 10240;
 constexpr int kDmaMaxParts = 6144;  // tiles * split
 
@@ -428,7 +427,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // first copy; the 10 younger copies may still fly) and its constant
   // stores; the barrier makes every wave's W0, constants and vote visible.
   __shared__ uint32_t dma_vote[8];
-  __shared__ uint32_t dma_flags[8];  // split-K: [0] arrival, [1] this part's mode, [2 + kk] part kk's mode
+  __shared__ uint32_t dma_flags[2];  // split-K: [0] arrival word, [1] this part parks through the L2
   const bool wave_ok = __builtin_amdgcn_ballot_w64(!ok) == 0;
   if (lane == 0) dma_vote[wave] = wave_ok ? 1u : 0u;
   asm volatile("" ::: "memory");
@@ -521,19 +520,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     default: reduce(std::integral_constant<int, 3>{}); break;
   }
 
-  // 6. Split K.  A workgroup parks its partial tile and counts its arrival
-  //    (counters[t]) while the stores are in flight.  Any but the last to
-  //    arrive then waits for its stores and marks its part parked; the last
-  //    waits until every other part is parked -- those workgroups have
-  //    arrived, so they run and finish their stores: the wait ends -- and
-  //    adds the parts in k-part order, so the result does not depend on
-  //    arrival order, then clears the tile's words for the next launch.
-  //    Parking: when every part of the tile runs on this XCD, through its
-  //    L2 (plain stores and loads); otherwise with the sc1 cache policy
-  //    (written through to, and read from, the memory side, as agent-scope
-  //    atomics are).  The parked mark says which, so the reader always
-  //    reads a part the way it was written.  Every store of a workgroup is
-  //    complete (s_waitcnt, then the barrier) before its part is marked.
+  // 6. Split K.  A workgroup parks its partial tile, waits until every
+  //    store is complete (s_waitcnt, then the barrier) and only then counts
+  //    its arrival (counters[t]), adding bit 8 + kh when it parked through
+  //    its L2.  The last to arrive (count split - 1) thus finds every other
+  //    part complete; it adds the parts in k-part order, so the result does
+  //    not depend on arrival order, then clears the tile's words for the
+  //    next launch.  Parking: when every part of the tile runs on this XCD,
+  //    through its L2 (plain stores and loads); otherwise with the sc1 cache
+  //    policy (written through to, and read from, the memory side, as
+  //    agent-scope atomics are).  The arrival bits say which, so the reader
+  //    always reads a part the way it was written.
   if (split > 1) {
     constexpr int SC1 = 16;  // cache-policy bit sc1
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
@@ -553,29 +550,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         else
           __builtin_amdgcn_raw_buffer_store_b128(v, pr, off(kh, r, q), 0, SC1);
       }
-    unsigned int* ready = counters + kDmaReadyOffset + t * split;
-    if (tid == 0) dma_flags[0] = __hip_atomic_fetch_add(&counters[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // every store of this thread complete
     __syncthreads();
-    if (dma_flags[0] != (unsigned int)(split - 1)) {
-      __builtin_amdgcn_s_waitcnt(0);  // every store of this thread complete
-      __syncthreads();
-      if (tid == 0) __hip_atomic_store(&ready[kh], local ? 2u : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return;
-    }
-    if (tid == 0) {
-      for (int kk = 0; kk < split; ++kk) {
-        if (kk == kh) continue;
-        // Bounded as a safety net only: the parts waited for are from
-        // workgroups that have arrived and have nothing left to wait for.
-        uint32_t mode = 0u;
-        for (int spin = 0; spin < (1 << 26) && mode == 0u; ++spin) {
-          mode = __hip_atomic_load(&ready[kk], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if (mode == 0u) __builtin_amdgcn_s_sleep(1);
-        }
-        dma_flags[2 + kk] = mode;
-      }
-    }
+    if (tid == 0)
+      dma_flags[0] = __hip_atomic_fetch_add(&counters[t], 1u + (local ? (256u << kh) : 0u), __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
+    if ((dma_flags[0] & 255u) != (unsigned int)(split - 1)) return;
+    const uint32_t l2_parts = dma_flags[0] >> 8;  // parked through this XCD's L2 (all parts run on it)
     // Part by part in k order; all 8 loads of a part are in flight at once.
     f32x4 sum[8];
     for (int kk = 0; kk < split; ++kk) {
@@ -585,7 +567,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int i = 0; i < 8; ++i)
           pv[i] = f32x4{res[i >> 2][4 * (i & 3)], res[i >> 2][4 * (i & 3) + 1], res[i >> 2][4 * (i & 3) + 2],
                         res[i >> 2][4 * (i & 3) + 3]};
-      } else if (dma_flags[2 + kk] == 2u) {
+      } else if ((l2_parts >> kk) & 1u) {
 #pragma unroll
         for (int i = 0; i < 8; ++i)
           pv[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off(kk, i >> 2, i & 3), 0, 0));
@@ -603,10 +585,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int e = 0; e < 4; ++e) res[i >> 2][4 * (i & 3) + e] = sum[i][e];
     if (tid == 0) {
       __hip_atomic_store(&counters[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      for (int kk = 0; kk < split; ++kk) {
-        __hip_atomic_store(&ready[kk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int kk = 0; kk < split; ++kk)
         __hip_atomic_store(&counters[kDmaXccOffset + t * split + kk], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
     }
   }
 
@@ -655,7 +635,7 @@ bool qmm_dma_fits(int m, int n, int k, int gs, int bits, int split) {
   if (k / split / gs > 8 * 4 * DMAXB) return false;
   if (dma_lds(k, gs, split) > (size_t)DLDS_MAX) return false;
   const uint64_t tiles = (uint64_t)((m + DBM - 1) / DBM) * ((n + DBN - 1) / DBN);
-  if (split > 1 && (tiles > (uint64_t)kDmaReadyOffset || tiles * split > (uint64_t)kDmaMaxParts)) return false;
+  if (split > 1 && (tiles > (uint64_t)kDmaMaxTiles || tiles * split > (uint64_t)kDmaMaxParts)) return false;
   const uint64_t xb = (uint64_t)m * k * 2, wb = (uint64_t)(n + DBN) * k / 2, yb = (uint64_t)m * n * 2;
   return xb < (1ull << 31) && wb < (1ull << 31) && yb < (1ull << 31);
 }

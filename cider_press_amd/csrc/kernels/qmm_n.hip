@@ -165,14 +165,14 @@ __global__ __launch_bounds__(256) void qmm_n_reduce_kernel(const float* __restri
 // constants (exact zeros).  The 32 row slots are added through LDS in slot
 // order.  With K split over parts the parts meet in the session scratch:
 // each stores its 256 sums with the sc1 policy (written through to the
-// memory side), counts its arrival on the column block's counter, waits for
-// its stores and sets its ready word; the last arriver waits for the other
-// parts' ready words, loads their sums with sc1 and adds the parts in part
-// order, then clears the block's words for the next launch.
+// memory side), waits until every store is acknowledged and only then
+// counts its arrival on the column block's counter; the last arriver (the
+// count it read is parts - 1) therefore finds every other part complete,
+// loads their sums with sc1, adds the parts in part order and clears the
+// counter for the next launch.
 // ---------------------------------------------------------------------------
 constexpr int QV_COLS = 256, QV_SLOTS = 32, QV_MAX_PARTS = 64;
-constexpr int kQvReady = 4096;     // ready words, after the per-block arrival counters (32-bit words)
-constexpr int kQvMaxWords = 6144;  // blocks * parts ready words
+constexpr int kQvMaxWords = 6144;  // column blocks * parts with K split (counters of blocks < 4096)
 
 __device__ __forceinline__ uint32_t half_of(uint32_t word, uint32_t hi) { return hi ? word >> 16 : word & 0xffffu; }
 
@@ -305,33 +305,18 @@ __global__ __launch_bounds__(256) void qvm_kernel(const uint32_t* __restrict__ w
         (void*)(partial + (size_t)blockIdx.x * parts * QV_COLS), 0, parts * QV_COLS * 4, 0x00020000);
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), pr, (uint32_t)(kp * QV_COLS + tid) * 4u, 0,
                                           SC1);
-    unsigned int* ready = counters + kQvReady + blockIdx.x * parts;
+    // Arrive only once every thread's store is acknowledged by the memory
+    // side: the last arriver then reads every part without waiting.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
     if (tid == 0)
       arrived = __hip_atomic_fetch_add(&counters[qv_counter(blockIdx.x)], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (arrived != (unsigned int)(parts - 1)) {
-      __builtin_amdgcn_s_waitcnt(0);  // this thread's store acknowledged by the memory side
-      __syncthreads();
-      if (tid == 0) __hip_atomic_store(&ready[kp], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return;
-    }
-    if (tid < 64) {
-      // Bounded as a safety net only: every other part has arrived and has
-      // nothing left to wait for before it sets its ready word.
-      const bool mine = tid < parts && tid != kp;
-      uint32_t r = mine ? 0u : 1u;
-      for (int spin = 0; spin < (1 << 24); ++spin) {
-        if (r == 0u) r = __hip_atomic_load(&ready[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (__ballot(r == 0u) == 0ull) break;
-        __builtin_amdgcn_s_sleep(1);
-      }
-    }
-    __syncthreads();
+    if (arrived != (unsigned int)(parts - 1)) return;
     v = parts <= 16   ? qv_sum_parts<16>(pr, parts, kp, tid, v)
         : parts <= 32 ? qv_sum_parts<32>(pr, parts, kp, tid, v)
                       : qv_sum_parts<QV_MAX_PARTS>(pr, parts, kp, tid, v);
     if (tid == 0) __hip_atomic_store(&counters[qv_counter(blockIdx.x)], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (tid < parts) __hip_atomic_store(&ready[tid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   const int col = n0 + tid;
   if (col < n) y[col] = TT::from_f32(v);

@@ -50,11 +50,10 @@ constexpr int SUW = 2;             // most units of one wave per chunk
 constexpr int SMAXSPLIT = 16;      // most K parts per tile
 constexpr int SXMAX = 128 * 1024;  // most LDS bytes of the activation tile
 
-// Split-K words in the scratch head (all zero between launches): arrival
-// count per tile [t]; per part how it was parked [kSmallReady + t*split + kk]
-// (0 not yet, 1 memory side, 2 through this XCD's L2); the XCD each part
-// runs on, plus one, [kSmallXcc + t*split + kk].
-constexpr int kSmallReady = 4096;
+// Split-K words in the scratch head (all zero between launches): per tile
+// [t] the arrivals (low 8 bits) and, bit 8 + kk, part kk parked through its
+// XCD's L2; the XCD each part runs on, plus one, [kSmallXcc + t*split + kk].
+constexpr int kSmallMaxTiles = 4096;
 constexpr int kSmallXcc = 10240;
 constexpr int kSmallMaxParts = 6144;
 constexpr size_t kSmall1Lds = 8 * 16384 + 7 * 64 * 16;  // per-wave activation pieces + parked K slices
@@ -68,7 +67,7 @@ __global__ __launch_bounds__(512) void qmm_small_kernel(const uint32_t* __restri
                                                         int tiles, float* __restrict__ part,
                                                         unsigned int* __restrict__ counters, int xdma) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  __shared__ uint32_t flags[2 + SMAXSPLIT];
+  __shared__ uint32_t flags[2];
   constexpr int R = 16 * MB;      // activation rows of the tile
   constexpr int NB = 16 * MB;     // columns of the tile
   constexpr int NKS = 8 / MB;     // K slices
@@ -238,14 +237,14 @@ __global__ __launch_bounds__(512) void qmm_small_kernel(const uint32_t* __restri
   }
 
   // 5. Split K: the prefill kernel's exchange.  A workgroup parks its partial
-  //    tile and counts its arrival while the stores are in flight; any but
-  //    the last then waits for its stores and marks its part parked; the
-  //    last waits for every other part (they have all arrived, so the wait
-  //    ends) and adds the parts in part order.  Parts of workgroups that
-  //    found every part of the tile on their XCD go through its L2 (plain
-  //    stores and loads), others with the sc1 policy (written through to,
-  //    and read from, the memory side, as agent-scope atomics are); the
-  //    parked mark says which.  Lane kk of wave 0 handles part kk's words.
+  //    tile, waits until every store is complete and only then counts its
+  //    arrival, adding bit 8 + kp when it parked through its L2; the last
+  //    arriver (count split - 1) thus finds every other part complete and
+  //    adds the parts in part order.  Parts of workgroups that found every
+  //    part of the tile on their XCD go through its L2 (plain stores and
+  //    loads), others with the sc1 policy (written through to, and read
+  //    from, the memory side, as agent-scope atomics are).  Lane kk of
+  //    wave 0 reads part kk's XCD word.
   if (split > 1) {
     constexpr int SC1 = 16;
     if (wave == 0) {
@@ -269,35 +268,20 @@ __global__ __launch_bounds__(512) void qmm_small_kernel(const uint32_t* __restri
         else
           __builtin_amdgcn_raw_buffer_store_b128(v4, pr, off(kp, mb), 0, SC1);
       }
-    unsigned int* ready = counters + kSmallReady + t * split;
-    if (tid == 0) flags[0] = __hip_atomic_fetch_add(&counters[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // every store of this thread complete
     __syncthreads();
-    if (flags[0] != (unsigned int)(split - 1)) {
-      __builtin_amdgcn_s_waitcnt(0);  // every store of this thread complete
-      __syncthreads();
-      if (tid == 0) __hip_atomic_store(&ready[kp], local ? 2u : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return;
-    }
-    if (wave == 0) {
-      // Bounded as a safety net only: the parts waited for belong to
-      // workgroups that have arrived and have nothing left to wait for.
-      uint32_t mode = 2u;
-      const bool mine = lane < split && lane != kp;
-      if (mine) mode = 0u;
-      for (int spin = 0; spin < (1 << 24); ++spin) {
-        if (mine && mode == 0u)
-          mode = __hip_atomic_load(&ready[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (__ballot(mode == 0u) == 0ull) break;
-        __builtin_amdgcn_s_sleep(1);
-      }
-      if (lane < split) flags[2 + lane] = mode;
-      const bool all_l2 = __ballot(lane < split && mode != 2u) == 0ull;
-      if (lane == 0) flags[1] = all_l2 ? 1u : 0u;
-    }
+    if (tid == 0)
+      flags[0] = __hip_atomic_fetch_add(&counters[t], 1u + (local ? (256u << kp) : 0u), __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
+    if ((flags[0] & 255u) != (unsigned int)(split - 1)) return;
+    // Parts parked through the L2: a part parks there only when all parts,
+    // this one included, run on its XCD.
+    const uint32_t l2_parts = flags[0] >> 8;
+    const uint32_t others = ((1u << split) - 1u) & ~(1u << kp);
     if (ks == 0) {
       f32x4 sum[MB];
-      if (flags[1] != 0u) {
+      if (l2_parts == others) {
         // Every part through this L2: four parts' loads in flight at a time.
         for (int k4 = 0; k4 < split; k4 += 4) {
           f32x4 pv[4][MB];
@@ -322,7 +306,7 @@ __global__ __launch_bounds__(512) void qmm_small_kernel(const uint32_t* __restri
           for (int mb = 0; mb < MB; ++mb) {
             if (kk == kp)
               pv[mb] = acc[mb];
-            else if (flags[2 + kk] == 2u)
+            else if ((l2_parts >> kk) & 1u)
               pv[mb] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off(kk, mb), 0, 0));
             else
               pv[mb] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off(kk, mb), 0, SC1));
@@ -336,10 +320,8 @@ __global__ __launch_bounds__(512) void qmm_small_kernel(const uint32_t* __restri
     }
     if (wave == 0) {
       if (lane == 0) __hip_atomic_store(&counters[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (lane < split) {
-        __hip_atomic_store(&ready[lane], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane < split)
         __hip_atomic_store(&counters[kSmallXcc + t * split + lane], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
     }
   }
 
@@ -572,7 +554,7 @@ SmallPlan qmm_small_plan(const QuantArgs& q, int m, int n, int k, int cu_count, 
     if (ku % d != 0 || (f_split && d != f_split)) continue;
     const int c = chunks(d);
     if (c == 0) continue;
-    if (d > 1 && (tiles > kSmallReady || tiles * d > kSmallMaxParts || small_scratch(tiles, d, mb) > scratch_cap))
+    if (d > 1 && (tiles > kSmallMaxTiles || tiles * d > kSmallMaxParts || small_scratch(tiles, d, mb) > scratch_cap))
       continue;
     best = d;
     best_c = c;
