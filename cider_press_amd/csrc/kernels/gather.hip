@@ -28,8 +28,9 @@
 // dependent round trips on a memory system not yet loaded by the stream);
 // the first weight steps are requested right after the activation loads.
 // Activation layout in LDS: [unit][16-row block][row][16 slots of 16 bytes],
-// slot s of row i stored at slot s ^ (i % 16) (the 16 rows of an MFMA read 16
-// distinct slots).  Weights stream from HBM exactly once per pass and
+// slot s of row i stored at slot s ^ key(i % 16), key(r) = r with its 2-bit
+// halves swapped, so that both lanes 16p .. 16p+15 and lanes p, p+4, ...,
+// p+60 of an MFMA operand read touch 16 distinct slots (no bank conflicts).  Weights stream from HBM exactly once per pass and
 // activations are read from L2 once per workgroup, so the kernel runs at the
 // weight stream's rate for routings with up to R rows per expert (more rows:
 // more passes).
@@ -352,6 +353,13 @@ __device__ __forceinline__ int wave_lower_bound(const uint32_t* __restrict__ a, 
   return lo;
 }
 
+// XOR key of row r (0..15) in the activation layout: the row's 2-bit halves
+// swapped.  With the row itself as the key, lanes p, p+4, ..., p+60 (rows
+// p, p+4, p+8, p+12 of the four chunk groups) meet in 4 slots, and
+// SQ_LDS_BANK_CONFLICT counted 4 cycles per 16-byte operand read; with the
+// swapped key it counts none.
+__device__ __forceinline__ int gx_key(int r) { return ((r & 3) << 2) | (r >> 2); }
+
 __device__ __forceinline__ int wave_isum(int v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -514,8 +522,8 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
   }
 
   // LDS offsets of this lane's A pieces: 16-byte piece i of chunk 4u + g of
-  // row nl of a block is slot (4g + i) ^ nl of the row (unit u, block mb at
-  // (u * MB + mb) * 4096 bytes).
+  // row nl of a block is slot (4g + i) ^ key(nl) of the row (unit u, block mb
+  // at (u * MB + mb) * 4096 bytes).
   GxCtx cx;
   cx.T = T;
   cx.units = units;
@@ -523,7 +531,7 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
   cx.g = g;
   cx.sel = gx_sb_sel<TT>(g);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) cx.aoff[i] = (uint32_t)nl * 256u + (uint32_t)(((4 * g + i) ^ nl) * 16);
+  for (int i = 0; i < 4; ++i) cx.aoff[i] = (uint32_t)nl * 256u + (uint32_t)(((4 * g + i) ^ gx_key(nl)) * 16);
   cx.xs = xs;
   cx.col0 = col0;
   cx.n = n;
@@ -604,7 +612,7 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
           const int i = ii[h], q = qq[h];
           const int r16 = i & 15;
           const uint32_t off = (uint32_t)((q >> 4) * MB + (i >> 4)) * 4096u + (uint32_t)r16 * 256u +
-                               (uint32_t)(((q & 15) ^ r16) * 16);
+                               (uint32_t)(((q & 15) ^ gx_key(r16)) * 16);
           *reinterpret_cast<u32x4*>(xs + off) = interleave_x<BITS>(v[h]);
         }
       }
