@@ -294,24 +294,34 @@ constexpr int kLeanXItems = 8;   // 16-B activation items per lane (K <= 16384)
 constexpr int kLeanQuads = 8;    // 8-B scale/bias quads per lane (wave's groups per row <= 128)
 
 // Per-wave LDS: activations (256 B per step and row) then constants [16][GW + 1].
-__host__ __device__ constexpr size_t lean_wave_lds(int nsteps, int gs_shift, int rows = 1) {
-  return (size_t)256 * nsteps * rows + (size_t)16 * ((size_t)nsteps * (128 >> gs_shift) + 1) * 16;
+__host__ __device__ constexpr size_t lean_wave_lds(int nsteps, int gs_shift, int rows = 1, int cw = 16) {
+  return (size_t)256 * nsteps * rows + (size_t)16 * ((size_t)nsteps * (128 >> gs_shift) + 1) * cw;
 }
 
 // MR > 1: xbase holds the lane's slice-0 address; slice i of step j sits at
 // xbase + xsw[i] + j * STEP_X (per-lane swizzled offsets of its row).
-template <typename TT, int BITS, int GS_SHIFT, int PF, bool ONE, bool FAST, int MR = 1>
+// CW: bytes per group's constants, 16 (s, b, b - 1024 s, b - 64 s) or 8
+// (s, b; the other two computed per step, the same fmaf).
+template <typename TT, int BITS, int GS_SHIFT, int PF, bool ONE, bool FAST, int MR = 1, int CW = 16>
 __device__ __forceinline__ f32x4 lean_stream(__amdgpu_buffer_rsrc_t wr, uint32_t voff, int nsteps,
                                              const unsigned char* cbase, const unsigned char* xbase,
                                              uint32_t (&buf)[PF][BITS], const int* xsw = nullptr) {
   constexpr int CB = BITS * 4;             // bytes per 32-element chunk
   constexpr int STEP_W = 4 * CB;           // weight bytes a lane group advances per step
-  constexpr int STEP_C = (128 >> GS_SHIFT) * 16;  // constants bytes per step
+  constexpr int STEP_C = (128 >> GS_SHIFT) * CW;  // constants bytes per step
   constexpr int STEP_X = 4 * 64;           // activation bytes per step (4 chunks x 32 x 2 B)
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   auto step = [&](const uint32_t* cur, int j) {
-    const f32x4 gc = *reinterpret_cast<const f32x4*>(cbase + j * STEP_C);
-    const float sc = gc[0], b = gc[1], c0 = gc[2], c1 = gc[3];
+    float sc, b, c0, c1;
+    if constexpr (CW == 16) {
+      const f32x4 gc = *reinterpret_cast<const f32x4*>(cbase + j * STEP_C);
+      sc = gc[0]; b = gc[1]; c0 = gc[2]; c1 = gc[3];
+    } else {
+      const f32x2 gc = *reinterpret_cast<const f32x2*>(cbase + j * STEP_C);
+      sc = gc[0]; b = gc[1];
+      c0 = FAST ? fmaf(-1024.f, sc, b) : 0.f;
+      c1 = FAST ? fmaf(-64.f, sc, b) : 0.f;
+    }
     const float s16 = sc * 0.0625f;
     if constexpr (MR == 1) {
       const u32x4* xa = reinterpret_cast<const u32x4*>(xbase + j * STEP_X);
@@ -499,8 +509,9 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_lean_kernel(const uint32_t* __
 // at slot s ^ r, so the 16 A rows of one MFMA read 16 distinct slots.  Rows
 // past M are not read: their A rows only feed output rows that are never
 // stored.  NST steps per wave (K = 128 * WAVES * NST); at most 16
-// activation items per lane (M * NST <= 64).
-template <typename TT, int BITS, int GS_SHIFT, int WAVES, int NST, bool BATCH>
+// activation items per lane (M * NST <= 64).  CW: bytes of a group's
+// constants in LDS (16, or 8 where the four-float form does not fit).
+template <typename TT, int BITS, int GS_SHIFT, int WAVES, int NST, bool BATCH, int CW = 16>
 __global__ __launch_bounds__(64 * WAVES) void qmm_lean_rows_kernel(const uint32_t* __restrict__ w,
                                                                     const uint16_t* __restrict__ scales,
                                                                     const uint16_t* __restrict__ biases,
@@ -527,9 +538,9 @@ __global__ __launch_bounds__(64 * WAVES) void qmm_lean_rows_kernel(const uint32_
   const int rows = min(m, 16);
   const int RB = 256 * nsteps;  // bytes of one activation row in a wave's region
   const uint32_t rowbytes = (uint32_t)k * BITS / 8;
-  const size_t wlds = lean_wave_lds(nsteps, GS_SHIFT, rows);
+  const size_t wlds = lean_wave_lds(nsteps, GS_SHIFT, rows, CW);
   unsigned char* xw = smem + (size_t)wave * wlds;
-  f32x4* cw = reinterpret_cast<f32x4*>(xw + (size_t)RB * rows);  // [16][GW + 1]
+  unsigned char* cw = xw + (size_t)RB * rows;  // [16][GW + 1] entries of CW bytes
   f32x4* red = reinterpret_cast<f32x4*>(smem + (size_t)WAVES * wlds);  // [WAVES][64]
 
   const __amdgpu_buffer_rsrc_t wr =
@@ -586,11 +597,18 @@ __global__ __launch_bounds__(64 * WAVES) void qmm_lean_rows_kernel(const uint32_
   for (int t = 0; t < kLeanQuads; ++t) {
     const int cq = (lane & 3) + 4 * t;
     if (4 * t < quads && cq < quads) {
-      f32x4* dst = cw + cr * cwp + cq * 4;
+      unsigned char* dst = cw + (size_t)(cr * cwp + cq * 4) * CW;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        dst[2 * h] = group_consts<TT>(sv[t][h] & 0xffffu, bv[t][h] & 0xffffu);
-        dst[2 * h + 1] = group_consts<TT>(sv[t][h] >> 16, bv[t][h] >> 16);
+        if constexpr (CW == 16) {
+          reinterpret_cast<f32x4*>(dst)[2 * h] = group_consts<TT>(sv[t][h] & 0xffffu, bv[t][h] & 0xffffu);
+          reinterpret_cast<f32x4*>(dst)[2 * h + 1] = group_consts<TT>(sv[t][h] >> 16, bv[t][h] >> 16);
+        } else {
+          reinterpret_cast<f32x2*>(dst)[2 * h] =
+              f32x2{TT::to_f32((uint16_t)(sv[t][h] & 0xffffu)), TT::to_f32((uint16_t)(bv[t][h] & 0xffffu))};
+          reinterpret_cast<f32x2*>(dst)[2 * h + 1] =
+              f32x2{TT::to_f32((uint16_t)(sv[t][h] >> 16)), TT::to_f32((uint16_t)(bv[t][h] >> 16))};
+        }
         fast_quick_add<TT>(fq, sv[t][h], bv[t][h]);
       }
     }
@@ -615,13 +633,14 @@ __global__ __launch_bounds__(64 * WAVES) void qmm_lean_rows_kernel(const uint32_
 
   // 4. Stream: lane (row r, group g) reads slice i of step j at
   //    xw + r * RB + j * 256 + ((4g + i) ^ r) * 16.
-  const unsigned char* cbase = reinterpret_cast<const unsigned char*>(cw + r * cwp + ((g * 32) >> GS_SHIFT));
+  const unsigned char* cbase = cw + (size_t)(r * cwp + ((g * 32) >> GS_SHIFT)) * CW;
   const unsigned char* xbase = xw + r * RB;
   int xsw[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) xsw[i] = ((4 * g + i) ^ r) << 4;
-  const f32x4 acc = fast ? lean_stream<TT, BITS, GS_SHIFT, PF, ONE, true, 16>(wr, voff, nsteps, cbase, xbase, buf, xsw)
-                         : lean_stream<TT, BITS, GS_SHIFT, PF, ONE, false, 16>(wr, voff, nsteps, cbase, xbase, buf, xsw);
+  const f32x4 acc =
+      fast ? lean_stream<TT, BITS, GS_SHIFT, PF, ONE, true, 16, CW>(wr, voff, nsteps, cbase, xbase, buf, xsw)
+           : lean_stream<TT, BITS, GS_SHIFT, PF, ONE, false, 16, CW>(wr, voff, nsteps, cbase, xbase, buf, xsw);
 
   // 5. The waves' K ranges in order; element i of lane (r, g) is output row
   //    4g + i, column n0 + r.
@@ -734,12 +753,12 @@ bool lean_fits(const QuantArgs& q, int n, int k, int waves) {
   return ((reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases)) & 7u) == 0;
 }
 
-template <typename TT, int BITS, int GS_SHIFT, int NST, bool BATCH>
+template <typename TT, int BITS, int GS_SHIFT, int NST, bool BATCH, int CW>
 hipError_t launch_rows_cfg(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
                            size_t lds, int count, const BatchArgs& ba) {
   if (lds > 64 * 1024) {
     static const hipError_t attr = [] {
-      const void* fn = reinterpret_cast<const void*>(&qmm_lean_rows_kernel<TT, BITS, GS_SHIFT, 8, NST, BATCH>);
+      const void* fn = reinterpret_cast<const void*>(&qmm_lean_rows_kernel<TT, BITS, GS_SHIFT, 8, NST, BATCH, CW>);
       hipFuncAttributes fa;
       hipError_t e = hipFuncGetAttributes(&fa, fn);
       if (e != hipSuccess) return e;
@@ -748,25 +767,41 @@ hipError_t launch_rows_cfg(hipStream_t s, const QuantArgs& q, const void* x, voi
     }();
     if (attr != hipSuccess) return attr;
   }
-  hipLaunchKernelGGL((qmm_lean_rows_kernel<TT, BITS, GS_SHIFT, 8, NST, BATCH>),
+  hipLaunchKernelGGL((qmm_lean_rows_kernel<TT, BITS, GS_SHIFT, 8, NST, BATCH, CW>),
                      dim3((unsigned)((n + 15) / 16), (unsigned)count), dim3(512), lds, s, q.w,
                      static_cast<const uint16_t*>(q.scales), static_cast<const uint16_t*>(q.biases),
                      static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), m, n, k, ba);
   return hipGetLastError();
 }
 
-template <typename TT, int BITS, int GS_SHIFT, bool BATCH>
-hipError_t launch_rows_gs(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
-                          size_t lds, int count, const BatchArgs& ba) {
+constexpr size_t kRowsLdsMax = 160 * 1024 - 1024;
+
+size_t rows_lds(int m, int k, int gs, int cw = 16) {
   const int nst = k / 1024;
-  if (nst == 4) return launch_rows_cfg<TT, BITS, GS_SHIFT, 4, BATCH>(s, q, x, y, m, n, k, lds, count, ba);
-  if (nst == 8) return launch_rows_cfg<TT, BITS, GS_SHIFT, 8, BATCH>(s, q, x, y, m, n, k, lds, count, ba);
-  return launch_rows_cfg<TT, BITS, GS_SHIFT, 16, BATCH>(s, q, x, y, m, n, k, lds, count, ba);
+  return (size_t)8 * lean_wave_lds(nst, shift_of(gs), std::min(m, 16), cw) + (size_t)8 * 64 * 16;
 }
 
-size_t rows_lds(int m, int k, int gs) {
+// Bytes per group's constants: 16 where they fit, else 8 at gs 32 (16 rows
+// at K = 4096: 170 KiB with 16, 156.5 KiB with 8).
+int rows_cw(int m, int k, int gs) { return rows_lds(m, k, gs) <= kRowsLdsMax || gs != 32 ? 16 : 8; }
+
+template <typename TT, int BITS, int GS_SHIFT, bool BATCH, int CW>
+hipError_t launch_rows_nst(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
+                           size_t lds, int count, const BatchArgs& ba) {
   const int nst = k / 1024;
-  return (size_t)8 * lean_wave_lds(nst, shift_of(gs), std::min(m, 16)) + (size_t)8 * 64 * 16;
+  if (nst == 4) return launch_rows_cfg<TT, BITS, GS_SHIFT, 4, BATCH, CW>(s, q, x, y, m, n, k, lds, count, ba);
+  if (nst == 8) return launch_rows_cfg<TT, BITS, GS_SHIFT, 8, BATCH, CW>(s, q, x, y, m, n, k, lds, count, ba);
+  return launch_rows_cfg<TT, BITS, GS_SHIFT, 16, BATCH, CW>(s, q, x, y, m, n, k, lds, count, ba);
+}
+
+template <typename TT, int BITS, int GS_SHIFT, bool BATCH>
+hipError_t launch_rows_gs(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
+                          int count, const BatchArgs& ba) {
+  if constexpr (GS_SHIFT == 5) {
+    if (rows_cw(m, k, q.gs) == 8)
+      return launch_rows_nst<TT, BITS, GS_SHIFT, BATCH, 8>(s, q, x, y, m, n, k, rows_lds(m, k, q.gs, 8), count, ba);
+  }
+  return launch_rows_nst<TT, BITS, GS_SHIFT, BATCH, 16>(s, q, x, y, m, n, k, rows_lds(m, k, q.gs), count, ba);
 }
 
 template <typename TT, int BITS>
@@ -841,7 +876,7 @@ bool qmv_rows_fits(const QuantArgs& q, int m, int n, int k, const void* x) {
   if (q.gs != 32 && q.gs != 64 && q.gs != 128) return false;
   if (m < 1 || m > 16 || n < 1 || (k != 4096 && k != 8192 && k != 16384)) return false;
   if (m * (k / 1024) > 64) return false;
-  if (rows_lds(m, k, q.gs) > 160 * 1024 - 1024) return false;
+  if (rows_lds(m, k, q.gs, rows_cw(m, k, q.gs)) > kRowsLdsMax) return false;
   if ((uint64_t)n * (uint64_t)k * q.bits / 8 >= (1ull << 31)) return false;
   if ((uint64_t)n * (uint64_t)(k / q.gs) * 2 >= (1ull << 31)) return false;
   if ((uint64_t)m * (uint64_t)k * 2 >= (1ull << 31)) return false;
@@ -852,13 +887,12 @@ bool qmv_rows_fits(const QuantArgs& q, int m, int n, int k, const void* x) {
 template <bool BATCH>
 hipError_t launch_rows_any(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k, int count,
                            const BatchArgs& ba) {
-  const size_t lds = rows_lds(m, k, q.gs);
   auto by_gs = [&](auto tt, auto bits) -> hipError_t {
     using TT = decltype(tt);
     constexpr int B = decltype(bits)::value;
-    if (q.gs == 32) return launch_rows_gs<TT, B, 5, BATCH>(s, q, x, y, m, n, k, lds, count, ba);
-    if (q.gs == 64) return launch_rows_gs<TT, B, 6, BATCH>(s, q, x, y, m, n, k, lds, count, ba);
-    return launch_rows_gs<TT, B, 7, BATCH>(s, q, x, y, m, n, k, lds, count, ba);
+    if (q.gs == 32) return launch_rows_gs<TT, B, 5, BATCH>(s, q, x, y, m, n, k, count, ba);
+    if (q.gs == 64) return launch_rows_gs<TT, B, 6, BATCH>(s, q, x, y, m, n, k, count, ba);
+    return launch_rows_gs<TT, B, 7, BATCH>(s, q, x, y, m, n, k, count, ba);
   };
   using B4 = std::integral_constant<int, 4>;
   using B8 = std::integral_constant<int, 8>;

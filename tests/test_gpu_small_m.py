@@ -113,13 +113,18 @@ def test_small_m_interleaved_shapes_keep_counters_clean(device, oracle):
     (13, 4096, 4096, 4, 128, "f16"),
     (16, 12288, 4096, 4, 64, "bf16"),
     (16, 4096, 4096, 8, 64, "bf16"),
+    (16, 4096, 4096, 4, 32, "bf16"),    # gs 32, 16 rows: (scale, bias) pairs in LDS, exact path
+    (15, 4096, 4096, 4, 32, "bf16"),    # the same layout, single-FMA path
+    (15, 2048, 4096, 8, 32, "f16"),
 ])
 def test_decode_layout_rows_parity(device, oracle, m, n, k, bits, gs, dtype):
     """Up to 16 rows on the decode kernel's layout (K of 4096, 8192 or 16384):
-    each wave stages M rows of its K range with the rows' slots swizzled."""
+    each wave stages M rows of its K range with the rows' slots swizzled.
+    At gs 32 with 15 or 16 rows the group constants are kept as (scale,
+    bias) pairs (the four-float form does not fit in LDS)."""
     rng = np.random.default_rng(m * 17 + n + k)
     w_q, s, b = make_weight(rng, n, k, gs, bits, dtype)
-    if bits == 4 and gs == 64:
+    if bits == 4 and (gs == 64 or m == 16):
         s[:, ::7] = 0  # zero scales: the per-group exact path inside one wave
     x = make_x(rng, m, k, dtype)
     print(f"decode rows m={m} n={n} k={k} bits={bits} gs={gs} {dtype}", flush=True)
