@@ -113,6 +113,28 @@ def test_dequantize_bit_exact(device, library, oracle, dtype, bits, gs):
     assert np.array_equal(got, oracle.dequantize(w_q, s, b, n, k, gs, bits, dtype))
 
 
+@pytest.mark.parametrize("n,k,bits,gs", [
+    (37, 96, 4, 32),       # 444 eight-element pieces: a partly filled last wave
+    (45, 160, 8, 32),
+    (4100, 8192, 4, 64),   # more pieces than one pass of the grid covers
+])
+def test_dequantize_bit_exact_ragged_and_large(device, library, oracle, n, k, bits, gs):
+    """Sizes that leave a wave's 256 pieces partly filled, and one larger
+    than a single pass of the grid-stride loop."""
+    rng = np.random.default_rng(n + k + bits)
+    w_q, s, b = make_weight(rng, n, k, gs, bits, "bf16", bias_noise=1e-3)
+    W, S, B = _upload_weight(device, w_q, s, b, "bf16")
+    out = device.upload(np.full(n * k + 64, 0x7FC0, np.uint16), "bf16")  # sentinel past the end
+    cmds = device.commands()
+    from cider_press_amd.kernels import _ptr
+    _lib.check(_lib.lib().cpq_affine_dequantize(cmds.handle, _lib.DTYPES["bf16"], _ptr(W), len(W), _ptr(S), len(S),
+                                                _ptr(B), len(B), _ptr(out), n * k, gs, bits))
+    cmds.commit_and_wait()
+    got = out.to_numpy()
+    assert np.array_equal(got[: n * k].reshape(n, k), oracle.dequantize(w_q, s, b, n, k, gs, bits, "bf16"))
+    assert (got[n * k:] == 0x7FC0).all()
+
+
 def test_dequantize_reference_entry_point_and_special_values(device, library, oracle):
     """affine_dequantize_bf16_gs64_b4 (dequantize.rs:58-137) at the reference
     test's 128x64 shape, with ties, tiny and large scales mixed in."""
