@@ -753,12 +753,12 @@ bool lean_fits(const QuantArgs& q, int n, int k, int waves) {
   return ((reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases)) & 7u) == 0;
 }
 
-template <typename TT, int BITS, int GS_SHIFT, int NST, bool BATCH, int CW>
+template <typename TT, int BITS, int GS_SHIFT, int NST, bool BATCH, int CW, int WAVES = 8>
 hipError_t launch_rows_cfg(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
                            size_t lds, int count, const BatchArgs& ba) {
   if (lds > 64 * 1024) {
     static const hipError_t attr = [] {
-      const void* fn = reinterpret_cast<const void*>(&qmm_lean_rows_kernel<TT, BITS, GS_SHIFT, 8, NST, BATCH, CW>);
+      const void* fn = reinterpret_cast<const void*>(&qmm_lean_rows_kernel<TT, BITS, GS_SHIFT, WAVES, NST, BATCH, CW>);
       hipFuncAttributes fa;
       hipError_t e = hipFuncGetAttributes(&fa, fn);
       if (e != hipSuccess) return e;
@@ -767,8 +767,8 @@ hipError_t launch_rows_cfg(hipStream_t s, const QuantArgs& q, const void* x, voi
     }();
     if (attr != hipSuccess) return attr;
   }
-  hipLaunchKernelGGL((qmm_lean_rows_kernel<TT, BITS, GS_SHIFT, 8, NST, BATCH, CW>),
-                     dim3((unsigned)((n + 15) / 16), (unsigned)count), dim3(512), lds, s, q.w,
+  hipLaunchKernelGGL((qmm_lean_rows_kernel<TT, BITS, GS_SHIFT, WAVES, NST, BATCH, CW>),
+                     dim3((unsigned)((n + 15) / 16), (unsigned)count), dim3(64 * WAVES), lds, s, q.w,
                      static_cast<const uint16_t*>(q.scales), static_cast<const uint16_t*>(q.biases),
                      static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), m, n, k, ba);
   return hipGetLastError();
@@ -797,6 +797,17 @@ hipError_t launch_rows_nst(hipStream_t s, const QuantArgs& q, const void* x, voi
 template <typename TT, int BITS, int GS_SHIFT, bool BATCH>
 hipError_t launch_rows_gs(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
                           int count, const BatchArgs& ba) {
+  // 8-bit rows at K = 4096 and up to 8 of them: 4 waves of 8 steps (two
+  // items per row and lane) instead of 8 waves of 4 (8-bit M = 8: 8.02 ->
+  // 6.91 us, M = 2: 6.43 -> 5.93 us at N = 4096); 4-bit measured 5-8 %
+  // faster with 8 waves.  CPQ_ROWS_WAVES = 4 or 8 forces the choice (tuning
+  // hook, read once per process).
+  static const int forced_w = env_int("CPQ_ROWS_WAVES", 0);
+  const bool four = forced_w == 4 || (forced_w != 8 && BITS == 8);
+  if (four && k == 4096 && m <= 8) {
+    const size_t lds4 = (size_t)4 * lean_wave_lds(8, GS_SHIFT, std::min(m, 16)) + (size_t)4 * 64 * 16;
+    return launch_rows_cfg<TT, BITS, GS_SHIFT, 8, BATCH, 16, 4>(s, q, x, y, m, n, k, lds4, count, ba);
+  }
   if constexpr (GS_SHIFT == 5) {
     if (rows_cw(m, k, q.gs) == 8)
       return launch_rows_nst<TT, BITS, GS_SHIFT, BATCH, 8>(s, q, x, y, m, n, k, rows_lds(m, k, q.gs, 8), count, ba);

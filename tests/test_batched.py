@@ -75,6 +75,7 @@ def _run_batched(device, library, oracle, shape, wbroad, xbroad, m, n, k, gs, bi
     ((2, 3), (True, True), (False, False), 8, 4096, 4096, 64, 4, "bf16"),  # shared weight: 48 rows, small-M kernel
     ((3,), (False,), (False,), 4, 1024, 4096, 64, 4, "bf16"),          # decode layout, batch in the grid
     ((5,), (False,), (False,), 16, 512, 8192, 128, 8, "f16"),          # decode layout, 16 rows, 8-bit
+    ((3,), (False,), (False,), 6, 1056, 4096, 64, 8, "bf16"),          # decode layout, 8-bit K = 4096: 4 waves
     ((2, 2), (False, True), (True, False), 3, 1024, 4096, 32, 4, "bf16"),  # grid, both operands broadcast on a dim
 ])
 def test_qmm_t_batched_parity(device, library, oracle, shape, wbroad, xbroad, m, n, k, gs, bits, dtype):

@@ -116,6 +116,8 @@ def test_small_m_interleaved_shapes_keep_counters_clean(device, oracle):
     (16, 4096, 4096, 4, 32, "bf16"),    # gs 32, 16 rows: (scale, bias) pairs in LDS, exact path
     (15, 4096, 4096, 4, 32, "bf16"),    # the same layout, single-FMA path
     (15, 2048, 4096, 8, 32, "f16"),
+    (8, 4096, 4096, 8, 32, "bf16"),     # 8-bit, K = 4096, up to 8 rows: 4 waves of 8 steps
+    (3, 2080, 4096, 8, 64, "f16"),      # the same, N not a multiple of 64
 ])
 def test_decode_layout_rows_parity(device, oracle, m, n, k, bits, gs, dtype):
     """Up to 16 rows on the decode kernel's layout (K of 4096, 8192 or 16384):
