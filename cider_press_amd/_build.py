@@ -45,6 +45,9 @@ COMMON = [
     f"--offload-arch={ARCH}",
     # Packed FP32 VALU ops stay off: the compiler must not form v_pk_*_f32.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Kernel arguments arrive in SGPRs before the wave starts (gfx950
+    # kernarg preloading), so a wave's first loads need no scalar round trip.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-I", os.path.join(ROOT, "include"),
 ]
 
