@@ -648,9 +648,13 @@ int qmm_dma_split(int m, int n, int k, int gs, int bits, int cu_count) {
   for (int split : {1, 2, 4}) {
     if (!qmm_dma_fits(m, n, k, gs, bits, split)) continue;
     // Makespan in k-units: rounds of one workgroup per CU, each K/split
-    // deep, plus the partial-tile exchange (about 4 stages) when split.
+    // deep plus a workgroup's fixed phases (prologue, K-quarter reduction,
+    // store: about 2000 k-units of loop time), plus the partial-tile
+    // exchange (about 4 stages) when split.  Fitted to measured splits:
+    // config 3a (M = 512, N = 4096) 1 / 2 / 4 parts 30.3 / 27.1 / 38.7 us,
+    // N = 12288 75.8 / 82.9 / 80.3 us, M = 2048 all within 2 %.
     const long rounds = (tiles * split + cus - 1) / cus;
-    const long cost = rounds * (k / split) + (split > 1 ? 512 : 0);
+    const long cost = rounds * (k / split + 2000) + (split > 1 ? 512 : 0);
     if (best == 0 || cost < best_cost) {
       best = split;
       best_cost = cost;

@@ -73,9 +73,10 @@ def test_noalloc_under_graph_capture(device, library):
 
 
 def test_noalloc_refuses_split_beyond_static_scratch(device, library):
-    # config 3b: a default session splits K over 2 with 48 MiB of partial
-    # tiles, more than the 16 MiB array.
-    m, n, k, gs = 512, 12288, 4096, 64
+    # K = 8192 at gs64 has 128 groups per row, more than one K range of the
+    # prefill kernel takes, so a default session splits K over 2: 32 MiB of
+    # partial tiles, more than the 16 MiB array.
+    m, n, k, gs = 512, 8192, 8192, 64
     W = device.alloc_buffer(n * k // 8, "u32")
     S = device.alloc_buffer(n * k // gs, "bf16")
     X = device.alloc_buffer(m * k, "bf16")
