@@ -386,74 +386,3 @@ int or_qmv_mlx(const uint16_t* x, size_t m, const uint32_t* w, const uint16_t* s
   free(q);
   return 0;
 }
-
-/* ------------------------------------------------------------------ */
-/* CPU baseline: dequantize-and-dot with fp32 accumulation, output T.    */
-/* Same semantics as the GPU path (T-rounded dequantized weights, fp32   */
-/* accumulate); multithreaded over N.  Timed by bench.py's cpu_baseline. */
-/* ------------------------------------------------------------------ */
-
-typedef struct {
-  const uint16_t* x; size_t m;
-  const uint32_t* w; const uint16_t* s; const uint16_t* b;
-  size_t n0, n1, n, k; int gs, bits, dtype;
-  uint16_t* y;
-} base_job;
-
-static void* baseline_worker(void* arg) {
-  base_job* j = (base_job*)arg;
-  size_t k = j->k;
-  float* xf = (float*)malloc(j->m * k * sizeof(float));
-  float* wrow = (float*)malloc(k * sizeof(float));
-  uint8_t* q = (uint8_t*)malloc(k);
-  for (size_t i = 0; i < j->m * k; ++i) xf[i] = to_f32(j->x[i], j->dtype);
-  size_t words_per_row = k * (size_t)j->bits / 32u;
-  size_t groups_per_row = k / (size_t)j->gs;
-  for (size_t r = j->n0; r < j->n1; ++r) {
-    if (j->bits == 4) {
-      const uint32_t* wr = j->w + r * words_per_row;
-      for (size_t wi = 0; wi < words_per_row; ++wi) {
-        uint32_t v = wr[wi];
-        for (int jj = 0; jj < 8; ++jj) q[wi * 8 + jj] = (uint8_t)((v >> (4 * jj)) & 15u);
-      }
-    } else {
-      or_unpack_row(j->w + r * words_per_row, j->bits, k, q);
-    }
-    for (size_t g = 0; g < groups_per_row; ++g) {
-      float s = to_f32(j->s[r * groups_per_row + g], j->dtype);
-      float b = to_f32(j->b[r * groups_per_row + g], j->dtype);
-      for (size_t i = g * (size_t)j->gs; i < (g + 1) * (size_t)j->gs; ++i)
-        wrow[i] = round_t(fmaf(s, (float)q[i], b), j->dtype);
-    }
-    for (size_t mi = 0; mi < j->m; ++mi) {
-      const float* xr = xf + mi * k;
-      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      size_t kk = 0;
-      for (; kk + 8 <= k; kk += 8)
-        for (int l = 0; l < 8; ++l) acc[l] += xr[kk + l] * wrow[kk + l];
-      float tot = 0.0f;
-      for (int l = 0; l < 8; ++l) tot += acc[l];
-      for (; kk < k; ++kk) tot += xr[kk] * wrow[kk];
-      j->y[mi * j->n + r] = from_f32(tot, j->dtype);
-    }
-  }
-  free(xf);
-  free(wrow);
-  free(q);
-  return NULL;
-}
-
-void or_cpu_baseline(const uint16_t* x, size_t m, const uint32_t* w, const uint16_t* scales,
-                     const uint16_t* biases, size_t n, size_t k, int gs, int bits, int dtype,
-                     uint16_t* y, int threads) {
-  threads = clamp_threads(threads, n);
-  pthread_t tid[64];
-  base_job jobs[64];
-  size_t per = (n + (size_t)threads - 1) / (size_t)threads;
-  for (int t = 0; t < threads; ++t) {
-    size_t n0 = (size_t)t * per, n1 = n0 + per < n ? n0 + per : n;
-    jobs[t] = (base_job){x, m, w, scales, biases, n0 < n ? n0 : n, n1, n, k, gs, bits, dtype, y};
-    pthread_create(&tid[t], NULL, baseline_worker, &jobs[t]);
-  }
-  for (int t = 0; t < threads; ++t) pthread_join(tid[t], NULL);
-}

@@ -59,7 +59,6 @@ def lib():
             _u16p, ctypes.c_void_p, _u32p, _sz, _u32p, _u16p, _u16p, _sz, _sz, _i, _i, _i, _f64p, _i]
         L.or_qmv_mlx.argtypes = [_u16p, _sz, _u32p, _u16p, _u16p, _sz, _sz, _i, _i, _i, _i, _f32p]
         L.or_qmv_mlx.restype = _i
-        L.or_cpu_baseline.argtypes = [_u16p, _sz, _u32p, _u16p, _u16p, _sz, _sz, _i, _i, _i, _u16p, _i]
         _lib = L
     return _lib
 
@@ -168,44 +167,42 @@ def qmv_mlx(x, w_q, scales, biases, m: int, n: int, k: int, gs: int, bits: int, 
     return y
 
 
-_AVX512_FLAGS = ("avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl")
+BASELINE_PATH = os.path.join(HERE, "_build", "libcpq_cpu_baseline.so")
+BASELINE_FORMS = {"scalar": 0, "avx2": 1, "avx512": 2}
 _base_lib = None
 
 
-def baseline_isa() -> str:
-    """"avx512" when the host CPU has the x86-64-v4 feature set, else "avx2"."""
-    try:
-        with open("/proc/cpuinfo") as fh:
-            for line in fh:
-                if line.startswith("flags"):
-                    flags = set(line.split(":", 1)[1].split())
-                    return "avx512" if all(f in flags for f in _AVX512_FLAGS) else "avx2"
-    except OSError:
-        pass
-    return "avx2"
-
-
 def _baseline_lib():
-    """The oracle build the CPU baseline runs: the AVX-512 twin on hosts with
-    AVX-512 (when built), else the portable AVX2 build."""
+    """The CPU baseline (oracle/cpu_baseline.c: scalar, AVX2 and AVX-512
+    forms of the dequantize-and-dot, dispatched at run time)."""
     global _base_lib
     if _base_lib is None:
-        path = os.path.join(HERE, "_build", "libcpq_oracle_avx512.so")
-        if baseline_isa() == "avx512" and os.path.exists(path):
-            L = ctypes.CDLL(path)
-            L.or_cpu_baseline.argtypes = [_u16p, _sz, _u32p, _u16p, _u16p, _sz, _sz, _i, _i, _i, _u16p, _i]
-            _base_lib = L
-        else:
-            _base_lib = lib()
+        if not os.path.exists(BASELINE_PATH):
+            build()
+        L = ctypes.CDLL(BASELINE_PATH)
+        L.cb_form_supported.argtypes = [_i]
+        L.cb_form_supported.restype = _i
+        L.cb_qmm.argtypes = [_u16p, _sz, _u32p, _u16p, _u16p, _sz, _sz, _i, _i, _i, _u16p, _i, _i]
+        L.cb_qmm.restype = _i
+        _base_lib = L
     return _base_lib
 
 
+def baseline_forms() -> list:
+    """The baseline forms this host runs, slowest first."""
+    L = _baseline_lib()
+    return [f for f, code in BASELINE_FORMS.items() if L.cb_form_supported(code)]
+
+
 def cpu_baseline(x, w_q, scales, biases, m: int, n: int, k: int, gs: int, bits: int, dtype: str,
-                 threads=None) -> np.ndarray:
+                 threads=None, form: str = "scalar") -> np.ndarray:
+    """T-rounded dequantized weights, fp32 accumulation, output T (raw bits)."""
     y = np.empty((m, n), np.uint16)
-    _baseline_lib().or_cpu_baseline(np.ascontiguousarray(x, np.uint16), m, np.ascontiguousarray(w_q, np.uint32),
-                          np.ascontiguousarray(scales, np.uint16), np.ascontiguousarray(biases, np.uint16),
-                          n, k, gs, bits, _DT[dtype], y, _threads(threads))
+    rc = _baseline_lib().cb_qmm(np.ascontiguousarray(x, np.uint16), m, np.ascontiguousarray(w_q, np.uint32),
+                                np.ascontiguousarray(scales, np.uint16), np.ascontiguousarray(biases, np.uint16),
+                                n, k, gs, bits, _DT[dtype], y, _threads(threads), BASELINE_FORMS[form])
+    if rc != 0:
+        raise ValueError(f"cpu_baseline: form {form!r} unavailable on this host or bad arguments")
     return y
 
 

@@ -271,9 +271,29 @@ def test_cpu_baseline_within_tolerance(oracle):
     w_q, s, b = make_weight(rng, n, k, gs, 4, "bf16")
     x = make_x(rng, m, k, "bf16")
     ref = oracle.qmm_ref(x, w_q, s, b, m, n, k, gs, 4, "bf16")
-    got = oracle.cpu_baseline(x, w_q, s, b, m, n, k, gs, 4, "bf16", threads=4)
-    rep = oracle.tolerance_report(got, ref, x, k, "bf16")
-    assert rep["ok"], rep
+    forms = oracle.baseline_forms()
+    assert "scalar" in forms
+    for form in forms:
+        got = oracle.cpu_baseline(x, w_q, s, b, m, n, k, gs, 4, "bf16", threads=4, form=form)
+        rep = oracle.tolerance_report(got, ref, x, k, "bf16")
+        assert rep["ok"], (form, rep)
+
+
+@pytest.mark.parametrize("dtype,bits,gs", [("f16", 4, 32), ("bf16", 8, 64), ("f16", 3, 64), ("bf16", 4, 128)])
+def test_cpu_baseline_forms_other_quantizations(oracle, dtype, bits, gs):
+    """Every baseline form (the SIMD ones fall back to scalar for widths other
+    than 4) against the oracle's float64 reference."""
+    from cider_press_amd.synthetic import make_weight, make_x
+
+    rng = np.random.default_rng(17)
+    m, n, k = 3, 96, 1024
+    w_q, s, b = make_weight(rng, n, k, gs, bits, dtype)
+    x = make_x(rng, m, k, dtype)
+    ref = oracle.qmm_ref(x, w_q, s, b, m, n, k, gs, bits, dtype)
+    for form in oracle.baseline_forms():
+        got = oracle.cpu_baseline(x, w_q, s, b, m, n, k, gs, bits, dtype, threads=3, form=form)
+        rep = oracle.tolerance_report(got, ref, x, k, dtype)
+        assert rep["ok"], (form, rep)
 
 
 def test_bf16_tolerance_rejects_factored_form(oracle):
