@@ -4,32 +4,53 @@
 Headline metric: qmv HBM GB/s at K=4096 x N=12288, 4-bit gs64,
 bf16 (config 2a) -> `value`; qmm TFLOP/s at M=512, N=K=4096 (config 3a) -> the
 `qmm` object.  A "step" is one kernel call over one batch of synthetic input
-already resident in HBM.  `--copies` independent weight copies are rotated
-so the working set (>= 450 MB for qmv) exceeds the 256 MB Infinity Cache;
-steps are captured into a HIP graph and replayed, bracketed by HIP events on
-the launch stream.  The CPU baseline leg times the oracle's multithreaded
-dequantize-and-dot on the host.
+already resident in HBM.
 
-    python bench.py [--steps K] [--warmup W] [--only qmv|qmm|all|configs] [--no-cpu] [--no-configs]
+Timing method (every row):
+  * weight copies are rotated so that the working set of each row is at
+    least ROTATE_BYTES (512 MiB = 2 x the 256 MB Infinity Cache); copy c holds
+    copy 0's packed words XOR a per-copy random word (uniform nibbles still)
+    and copy 0's scales and biases;
+  * `--steps` calls (S) are captured into one HIP graph and 2S calls into a
+    second; each graph is replayed once untimed, then `reps` times (the two
+    interleaved), each replay enqueued right behind a 512 MiB streaming read
+    (cache flush) and bracketed by HIP events on the launch stream, with no
+    host synchronisation in between: the host submits the replay while the
+    GPU reads, so host submission is not in the window;
+  * the figure is the marginal time of a step, (median T(2S) - median
+    T(S)) / S: a graph replay carries a fixed cost (about 11 us here) that
+    this removes, so the figure does not depend on S.  The fixed cost and the
+    plain replay mean per step are reported beside it.
+One command session serves the whole run.
 
-The line's "configs" object times the other configurations of the
-measurement table (cfg1, cfg2b, cfg3b/3c, cfg4 small-M sweep through the
-routed op, cfg5 routed experts) the same way.
+    python bench.py [--steps K] [--warmup W] [--only qmv|qmm|configs|ceiling|dense|copy] [--no-cpu]
+                    [--no-configs] [--no-graph]
+
+`--no-graph` encodes the timed calls directly on the stream (no graph
+capture); it is the form used for kernel traces of the whole table.
+
+The line also carries: the single-launch streaming-read ceiling of the
+headline bytes (best of several read designs and grids) and of every row's
+bytes; the launch floor (a one-workgroup read of 16 bytes per step); a dense
+bf16 GEMM anchor (torch.matmul, i.e. hipBLASLt, at the qmm shapes, same timing
+method, measurement only); the configs table (cfg1, cfg2b, cfg3b/3c, 8-bit
+prefill, cfg4 small-M sweep through the routed op, cfg5 routed experts incl.
+decode-shaped routing, the reference's own Qwen2.5-0.5B decode and M=39
+prefill shapes), each row checked against the oracle; and the CPU baseline.
 
 HBM traffic (`roofline.traffic`) comes from rocprofv3 counter runs of this
 same script, calibrated against a plain device copy of known size:
 
-    rocprofv3 --pmc FETCH_SIZE -d D1 -o run --output-format csv -- python3 bench.py
-    rocprofv3 --pmc WRITE_SIZE -d D2 -o run --output-format csv -- python3 bench.py
+    rocprofv3 --pmc FETCH_SIZE -d D1 -o run --output-format csv -- python3 bench.py --no-configs --no-cpu
+    rocprofv3 --pmc WRITE_SIZE -d D2 -o run --output-format csv -- python3 bench.py --no-configs --no-cpu
     rocprofv3 --pmc FETCH_SIZE -d D3 -o run --output-format csv -- python3 bench.py --only copy
     rocprofv3 --pmc WRITE_SIZE -d D4 -o run --output-format csv -- python3 bench.py --only copy
     python bench.py --pmc-summary D1 D2 D3 D4   # -> profiles/traffic.json
-
-`bench.py` reads profiles/traffic.json when it names the kernel being timed.
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -44,12 +65,30 @@ METRIC = "qmv HBM GB/s (%peak) K4096×N12288 4b; qmm TFLOPS (%MFMA peak) M=512"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 
-
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic.json")
 COPY_BYTES = 512 << 20         # calibration copy: 512 MiB read + 512 MiB written
+ROTATE_BYTES = 512 << 20       # per-row rotated working set: 2 x the 256 MB Infinity Cache
+FLUSH_BYTES = 512 << 20        # streaming read before each timed replay
 QMV_KERNEL = "qmv_lean_kernel<cpq::dev::BF16, 4"
 QMM_KERNEL = "qmm_dma_kernel<cpq::dev::BF16"
-COPY_KERNEL = "copy"
+
+# Published reference figures (Apple M4 Max, bf16, 4-bit gs64, effective
+# GB/s by the same byte formula): docs/inference/quantized-matmul.md:121-153.
+REF_QMV_SHAPES = (  # (K, N, label, x_len, published GB/s)
+    (896, 4864, "gate/up_proj", 896, 306.0),
+    (4864, 896, "down_proj", 4864, 272.0),
+    (896, 151936, "lm_head", 896, 464.0),
+    (896, 896, "q/o_proj", 896, 85.0),
+    (896, 128, "k/v_proj", 896, 13.0),
+    (1024, 896, "q/o_proj K-padded 896->1024", 896, 139.0),
+    (1024, 128, "k/v_proj K-padded 896->1024", 896, 22.0),
+)
+# The reference's prefill benchmark shapes: Qwen2.5-0.5B at M = 39
+# (crates/cider-press-kernels/tests/qmm_dispatch_bench.rs:33,150-159); no
+# published figure.
+REF_QMM_M = 39
+REF_QMM_SHAPES = ((896, 896, "q_proj"), (896, 128, "k_proj"), (896, 896, "o_proj"), (896, 4864, "gate/up"),
+                  (4864, 896, "down"), (896, 151936, "lm_head"))
 
 
 def algo_bytes(m, n, k, gs, bits, tsize=2):
@@ -57,80 +96,158 @@ def algo_bytes(m, n, k, gs, bits, tsize=2):
     return n * k * bits // 8 + 2 * n * (k // gs) * tsize + m * k * tsize + m * n * tsize
 
 
-def make_copies(dev, rng, copies, n, k, gs, bits, dtype):
-    from cider_press_amd.synthetic import from_bits, to_bits
-
-    out = []
-    host0 = None
-    for c in range(copies):
-        w = rng.integers(0, 2**32, size=(n, k * bits // 32), dtype=np.uint64).astype(np.uint32)
-        s = to_bits(rng.uniform(0.002, 0.02, size=(n, k // gs)).astype(np.float32), dtype)
-        b = to_bits(-float(1 << (bits - 1)) * from_bits(s, dtype), dtype)
-        if c == 0:
-            host0 = (w, s, b)
-        out.append((dev.upload(w.reshape(-1), "u32"), dev.upload(s.reshape(-1), dtype),
-                    dev.upload(b.reshape(-1), dtype)))
-    return out, host0
+def copies_for(copy_bytes, target=ROTATE_BYTES):
+    """Rotated copies so the working set is at least `target` bytes."""
+    return int(max(2, -(-target // max(int(copy_bytes), 1))))
 
 
-class Flusher:
-    """Evicts the 256 MB Infinity Cache (and L2) before a timed region with a
-    plain read of a 512 MiB buffer nothing else touches.  It reads, so it
-    leaves clean lines: a flush that wrote would have its dirty lines written
-    back to HBM during the timed region.  Without it the first weight copies
-    of the timed replay could still be cache-resident from the untimed one."""
+def reps_for(steps):
+    """Timed replays: at least 10, more for short graphs."""
+    return int(max(10, min(100, 2000 // max(steps, 1))))
 
-    def __init__(self, dev):
-        import ctypes
 
-        self.buf = dev.alloc_buffer(128 << 20, "u32")
-        self.sink = dev.alloc_buffer(1, "u32")
-        self.ptrs = (ctypes.c_void_p * 1)(self.buf.ptr)
-        self.lens = (ctypes.c_size_t * 1)(self.buf.byte_len)
+ORACLE_THREADS = min(16, os.cpu_count() or 1)
 
-    def flush(self, cmds):
-        import ctypes
 
+class Harness:
+    """One command session for the whole run, the cache-flush buffer, event
+    pairs and the graph timing method."""
+
+    def __init__(self, dev, use_graph=True):
         from cider_press_amd import _lib
 
-        _lib.check(_lib.lib().cpq_stream_read(cmds.handle, self.ptrs, self.lens, 1, ctypes.c_void_p(self.sink.ptr),
-                                              4096))
+        self.dev = dev
+        self.L = _lib.lib()
+        self._check = _lib.check
+        self.cmds = dev.commands()
+        self.use_graph = use_graph
+        self.flush_buf = dev.alloc_buffer(FLUSH_BYTES // 4, "u32")
+        self.sink = dev.alloc_buffer(64, "u32")
+        self._fp = (ctypes.c_void_p * 1)(self.flush_buf.ptr)
+        self._fl = (ctypes.c_size_t * 1)(self.flush_buf.byte_len)
+        self.events = []
 
+    def sync(self):
+        self.cmds.commit_and_wait()
 
-_FLUSHER = None
+    def eager(self, fn):
+        fn(self.cmds)
+        self.sync()
 
+    def flush(self):
+        """512 MiB streaming read: evicts the Infinity Cache and L2 and leaves
+        only clean lines (nothing is written back inside a timed window)."""
+        self._check(self.L.cpq_stream_read_variant(self.cmds.handle, self._fp, self._fl, 1,
+                                                   ctypes.c_void_p(self.sink.ptr), 4096, 1))
 
-def time_graph(dev, steps, warmup, encode_step):
-    """Capture `steps` calls in a graph, replay once untimed per warmup batch,
-    replay the timed graph once untimed, flush the caches, then time one
-    replay between HIP events on the launch stream."""
-    global _FLUSHER
-    from cider_press_amd.kernels import Event
+    def stream_read(self, cmds, ptrs, lens, n, nwg, variant):
+        self._check(self.L.cpq_stream_read_variant(cmds.handle, ptrs, lens, n, ctypes.c_void_p(self.sink.ptr),
+                                                   nwg, variant))
 
-    if _FLUSHER is None:
-        _FLUSHER = Flusher(dev)
-    cmds = dev.commands()
-    if warmup:
+    def _event_pairs(self, n):
+        from cider_press_amd.kernels import Event
+
+        while len(self.events) < n:
+            self.events.append((Event(), Event()))
+        return self.events[:n]
+
+    def _capture(self, steps, encode_step):
+        cmds = self.cmds
         cmds.begin_capture()
-        for i in range(warmup):
-            encode_step(cmds, i)
-        gw = cmds.end_capture()
-        gw.launch(cmds)
-        cmds.commit_and_wait()
-    cmds.begin_capture()
-    for i in range(steps):
-        encode_step(cmds, i)
-    g = cmds.end_capture()
-    g.launch(cmds)          # one untimed replay of the timed graph itself
-    _FLUSHER.flush(cmds)    # no weight copy starts the timed replay cache-resident
-    cmds.commit_and_wait()
-    e0, e1 = Event(), Event()
-    cmds.commit_and_wait()  # barrier: nothing in flight before the timed region
-    e0.record(cmds)
-    g.launch(cmds)
-    e1.record(cmds)
-    cmds.commit_and_wait()
-    return e0.elapsed_ms(e1) / steps
+        try:
+            for i in range(steps):
+                encode_step(cmds, i)
+        except BaseException:
+            try:
+                cmds.end_capture().close()
+            except Exception:
+                pass
+            raise
+        return cmds.end_capture()
+
+    def time(self, encode_step, steps, warmup, reps=None):
+        """Per-step time of `encode_step` as the marginal cost of a step: two
+        graphs of S and 2S steps are replayed `reps` times each (interleaved,
+        every replay behind the cache flush), and the per-step time is
+        (median T(2S) - median T(S)) / S.  A graph replay carries a fixed cost
+        of about 11 us on this device whatever it holds (launch of the graph,
+        measured with one-step graphs); the difference removes it, so the
+        figure does not depend on S.  The fixed cost and the plain replay
+        mean per step are reported beside it."""
+        reps = reps or reps_for(steps)
+        cmds = self.cmds
+        graphs = []
+        try:
+            runs = []
+            for s in (steps, 2 * steps):
+                if self.use_graph:
+                    g = self._capture(s, encode_step)
+                    graphs.append(g)
+                    runs.append(lambda g=g: g.launch(cmds))
+                else:
+                    runs.append(lambda s=s: [encode_step(cmds, i) for i in range(s)])
+            if warmup:
+                if self.use_graph:
+                    gw = self._capture(warmup, encode_step)
+                    graphs.append(gw)
+                    gw.launch(cmds)
+                else:
+                    for i in range(warmup):
+                        encode_step(cmds, i)
+            for run in runs:  # one untimed replay of each timed graph
+                run()
+            self.sync()
+            pairs = self._event_pairs(2 * reps)
+            for r in range(reps):
+                for j, run in enumerate(runs):
+                    e0, e1 = pairs[2 * r + j]
+                    self.flush()
+                    e0.record(cmds)
+                    run()
+                    e1.record(cmds)
+            self.sync()
+            t1 = sorted(pairs[2 * r][0].elapsed_ms(pairs[2 * r][1]) * 1e3 for r in range(reps))
+            t2 = sorted(pairs[2 * r + 1][0].elapsed_ms(pairs[2 * r + 1][1]) * 1e3 for r in range(reps))
+        finally:
+            self.sync()
+            for gr in graphs:
+                gr.close()
+        m1, m2 = t1[len(t1) // 2], t2[len(t2) // 2]
+        per = (m2 - m1) / steps
+        return {"us": per, "us_replay": m1 / steps, "fixed_us": m1 - per * steps,
+                "us_min": (t2[0] - t1[0]) / steps, "us_max": (t2[-1] - t1[-1]) / steps, "reps": reps,
+                "steps": steps}
+
+
+class Rotation:
+    """Rotated device copies of one quantized weight (or expert table): copy 0
+    from the generator, copy c its packed words XOR a per-copy random word."""
+
+    def __init__(self, dev, rng, n, k, gs, bits, dtype, bias_noise=0.0, copies=None):
+        from cider_press_amd.synthetic import make_weight
+
+        w, s, b = make_weight(rng, n, k, gs, bits, dtype, bias_noise=bias_noise)
+        self.host0 = (w, s, b)
+        self.copy_bytes = w.nbytes + s.nbytes + b.nbytes
+        self.n_copies = copies or copies_for(self.copy_bytes)
+        keys = rng.integers(1, 2**32, size=self.n_copies, dtype=np.uint64).astype(np.uint32)
+        Sd = dev.upload(s.reshape(-1), dtype)
+        Bd = dev.upload(b.reshape(-1), dtype)
+        self.copies = []
+        for c in range(self.n_copies):
+            wc = w if c == 0 else (w ^ keys[c])
+            # Scales and biases differ per copy in address only (same values:
+            # the fast-dequantization vote sees the same constants).
+            sc = Sd if c == 0 else dev.upload(s.reshape(-1), dtype)
+            bc = Bd if c == 0 else dev.upload(b.reshape(-1), dtype)
+            self.copies.append((dev.upload(wc.reshape(-1), "u32"), sc, bc))
+
+    def __getitem__(self, i):
+        return self.copies[i % self.n_copies]
+
+    @property
+    def working_set_mb(self):
+        return round(self.n_copies * self.copy_bytes / 2**20, 1)
 
 
 def parity_entry(rep, rows=None):
@@ -155,96 +272,187 @@ def check_rows(m):
     return np.array(sorted(rows))
 
 
-ORACLE_THREADS = min(16, os.cpu_count() or 1)
+def _timing(t):
+    return {"us": round(t["us"], 3), "us_replay": round(t["us_replay"], 3), "fixed_us": round(t["fixed_us"], 2),
+            "reps": t["reps"]}
 
 
-def bench_qmv(dev, lib, args, rng):
+class Ceiling:
+    """Single-launch streaming-read ceilings over rotated regions."""
+
+    GRIDS = (768, 1024, 2048, 4096)
+
+    def __init__(self, h):
+        self.h = h
+        self.best_variant = 1
+
+    def _regs(self, regions_per_copy):
+        regs = []
+        for rs in regions_per_copy:
+            ptrs = (ctypes.c_void_p * len(rs))(*[p for p, _ in rs])
+            lens = (ctypes.c_size_t * len(rs))(*[n for _, n in rs])
+            regs.append((ptrs, lens, len(rs)))
+        return regs
+
+    def measure(self, regions_per_copy, steps, warmup, variants=None, grids=None):
+        """Best per-step time over (variant, grid) of a plain read of the same
+        rotated regions, one launch per step."""
+        regs = self._regs(regions_per_copy)
+        variants = variants if variants is not None else (self.best_variant,)
+        grids = grids or self.GRIDS
+        table, best = {}, None
+        for v in variants:
+            for nwg in grids:
+                def step(c, i, v=v, nwg=nwg):
+                    ptrs, lens, n = regs[i % len(regs)]
+                    self.h.stream_read(c, ptrs, lens, n, nwg, v)
+
+                t = self.h.time(step, steps, warmup)
+                table[f"v{v}_wg{nwg}"] = round(t["us"], 3)
+                if best is None or t["us"] < best[0]:
+                    best = (t["us"], v, nwg)
+        return {"us": round(best[0], 3), "variant": best[1], "grid": best[2], "sweep_us": table}
+
+
+def _wsb_regions(rot, x_buf=None):
+    out = []
+    for W, S, B in rot.copies:
+        rs = [(W.ptr, W.byte_len), (S.ptr, S.byte_len), (B.ptr, B.byte_len)]
+        if x_buf is not None:
+            rs.append((x_buf.ptr, x_buf.byte_len))
+        out.append(rs)
+    return out
+
+
+def bench_qmv(h, lib, args, rng, ceil):
     from cider_press_amd.kernels import qmv as kqmv
     from cider_press_amd.synthetic import make_x
 
     n, k, gs, bits, dtype = 12288, 4096, 64, 4, "bf16"
-    copies, host0 = make_copies(dev, rng, args.copies, n, k, gs, bits, dtype)
+    rot = Rotation(h.dev, rng, n, k, gs, bits, dtype)
     x = make_x(rng, 1, k, dtype)
-    X = dev.upload(x.reshape(-1), dtype)
-    Y = dev.alloc_buffer(n, dtype)
+    X = h.dev.upload(x.reshape(-1), dtype)
+    Y = h.dev.alloc_buffer(n, dtype)
 
     def step(cmds, i):
-        W, S, B = copies[i % len(copies)]
-        kqmv.affine_qmv(cmds, lib, W, S, B, X, Y, k, gs, bits)
+        kqmv.affine_qmv(cmds, lib, *rot[i], X, Y, k, gs, bits)
 
     parity = None
     if not args.no_parity:
         from oracle import oracle as O  # checker only
 
-        cmds = dev.commands()
-        step(cmds, 0)
-        cmds.commit_and_wait()
-        ref = O.qmm_ref(x, *host0, 1, n, k, gs, bits, dtype, threads=ORACLE_THREADS)
+        h.eager(lambda c: step(c, 0))
+        ref = O.qmm_ref(x, *rot.host0, 1, n, k, gs, bits, dtype, threads=ORACLE_THREADS)
         parity = parity_entry(O.tolerance_report(Y.to_numpy().reshape(1, n), ref, x, k, dtype))
-    ms = time_graph(dev, args.steps, args.warmup, step)
+    t = h.time(step, args.steps, args.warmup)
     nbytes = algo_bytes(1, n, k, gs, bits)
-    gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"ms": ms, "gbs": gbs, "bytes": nbytes, "parity": parity, "host0": host0, "x": x,
-            "shape": (n, k, gs, bits), "copies": copies, "X": X}
+    # Ceiling: every read design x grid over the same rotated bytes.
+    c = ceil.measure(_wsb_regions(rot, X), args.steps, args.warmup,
+                     variants=range(h.L.cpq_stream_read_variant_count()))
+    ceil.best_variant = c["variant"]
+    c["what"] = ("plain streaming read of the same rotated copies (W, scales, biases, x) in one launch per "
+                 "step, best over read designs x grids")
+    c["bytes_read"] = sum(int(nb) for _, nb in _wsb_regions(rot, X)[0])
+    c["GB/s"] = round(c["bytes_read"] / (c["us"] * 1e-6) / 1e9, 1)
+    c["frac_of_peak"] = round(c["GB/s"] / HBM_PEAK_GBS, 4)
+    gbs = nbytes / (t["us"] * 1e-6) / 1e9
+    c["qmv_frac_of_ceiling"] = round(gbs / c["GB/s"], 4)
+    return {"t": t, "gbs": gbs, "bytes": nbytes, "parity": parity, "host0": rot.host0, "x": x,
+            "shape": (n, k, gs, bits), "copies": rot.n_copies, "working_set_mb": rot.working_set_mb,
+            "ceiling": c}
 
 
-def bench_qmm(dev, lib, args, rng):
+def bench_qmm(h, lib, args, rng):
     from cider_press_amd.kernels import qmm as kqmm
     from cider_press_amd.synthetic import make_x
 
     m, n, k, gs, bits, dtype = 512, 4096, 4096, 64, 4, "bf16"
-    copies, host0 = make_copies(dev, rng, args.copies, n, k, gs, bits, dtype)
+    rot = Rotation(h.dev, rng, n, k, gs, bits, dtype)
     x = make_x(rng, m, k, dtype)
-    X = dev.upload(x.reshape(-1), dtype)
-    Y = dev.alloc_buffer(m * n, dtype)
+    X = h.dev.upload(x.reshape(-1), dtype)
+    Y = h.dev.alloc_buffer(m * n, dtype)
 
     def step(cmds, i):
-        W, S, B = copies[i % len(copies)]
-        kqmm.affine_qmm_t(cmds, lib, W, S, B, X, Y, m, n, k, gs, bits)
+        kqmm.affine_qmm_t(cmds, lib, *rot[i], X, Y, m, n, k, gs, bits)
 
     parity = None
     if not args.no_parity:
         from oracle import oracle as O  # checker only
 
-        cmds = dev.commands()
-        step(cmds, 0)
-        cmds.commit_and_wait()
-        ref = O.qmm_ref(x, *host0, m, n, k, gs, bits, dtype, threads=ORACLE_THREADS)
+        h.eager(lambda c: step(c, 0))
+        ref = O.qmm_ref(x, *rot.host0, m, n, k, gs, bits, dtype, threads=ORACLE_THREADS)
         parity = parity_entry(O.tolerance_report(Y.to_numpy().reshape(m, n), ref, x, k, dtype))
-    ms = time_graph(dev, args.qmm_steps, args.warmup, step)
+    t = h.time(step, args.qmm_steps, args.warmup)
     flops = 2.0 * m * n * k
-    tflops = flops / (ms * 1e-3) / 1e12
-    return {"ms": ms, "tflops": tflops, "flops": flops, "bytes": algo_bytes(m, n, k, gs, bits),
-            "parity": parity}
+    return {"t": t, "tflops": flops / (t["us"] * 1e-6) / 1e12, "flops": flops,
+            "bytes": algo_bytes(m, n, k, gs, bits), "parity": parity, "copies": rot.n_copies,
+            "working_set_mb": rot.working_set_mb}
 
 
-def _weights(dev, rng, copies, n, k, gs, bits, dtype, bias_noise=0.0):
-    """Rotated device copies and the host arrays of copy 0 (the parity input)."""
-    from cider_press_amd.synthetic import make_weight
+def bench_dense(args, shapes=((512, 4096, 4096), (512, 12288, 4096), (2048, 4096, 4096), (2048, 12288, 4096))):
+    """Dense anchor: torch.matmul in bf16 (hipBLASLt on ROCm) on X[M,K] . W[N,K]^T,
+    rotated bf16 weights (>= 512 MiB), torch graph of `steps` calls, each timed
+    replay behind a 512 MiB read, median of the replays.  Measurement only:
+    nothing in the package uses it."""
+    import torch
 
-    out, host0 = [], None
-    for c in range(copies):
-        w, s, b = make_weight(rng, n, k, gs, bits, dtype, bias_noise=bias_noise)
-        if c == 0:
-            host0 = (w, s, b)
-        out.append((dev.upload(w.reshape(-1), "u32"), dev.upload(s.reshape(-1), dtype),
-                    dev.upload(b.reshape(-1), dtype)))
-    return out, host0
+    dev = "cuda"
+    steps = max(10, min(args.qmm_steps, 50))
+    reps = 10
+    rows = []
+    s = torch.cuda.Stream()
+    flush = torch.zeros(FLUSH_BYTES // 4, dtype=torch.int32, device=dev)
+    g0 = torch.Generator(device=dev)
+    g0.manual_seed(0)
+    for m, n, k in shapes:
+        wb = n * k * 2
+        copies = copies_for(wb)
+        X = torch.randn(m, k, device=dev, dtype=torch.bfloat16, generator=g0)
+        W0 = (torch.randn(n, k, device=dev, dtype=torch.bfloat16, generator=g0) * 0.02)
+        Ws = [W0] + [W0.clone() for _ in range(copies - 1)]
+        Y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+        with torch.cuda.stream(s):
+            for i in range(3):
+                torch.matmul(X, Ws[i % copies].t(), out=Y)
+        torch.cuda.synchronize()
+        gs_ = []
+        for n_steps in (steps, 2 * steps):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                for i in range(n_steps):
+                    torch.matmul(X, Ws[i % copies].t(), out=Y)
+            gs_.append(g)
+        with torch.cuda.stream(s):
+            for g in gs_:
+                g.replay()
+            ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in gs_]
+                  for _ in range(reps)]
+            for r in range(reps):
+                for g, (e0, e1) in zip(gs_, ev[r]):
+                    flush.sum()
+                    e0.record(s)
+                    g.replay()
+                    e1.record(s)
+        torch.cuda.synchronize()
+        t1 = sorted(ev[r][0][0].elapsed_time(ev[r][0][1]) * 1e3 for r in range(reps))
+        t2 = sorted(ev[r][1][0].elapsed_time(ev[r][1][1]) * 1e3 for r in range(reps))
+        us = (t2[reps // 2] - t1[reps // 2]) / steps
+        tf = 2.0 * m * n * k / (us * 1e-6) / 1e12
+        rows.append({"shape": f"X[{m},{k}] . W[{n},{k}]^T bf16", "m": m, "n": n, "k": k, "us": round(us, 3),
+                     "us_replay": round(t1[reps // 2] / steps, 3), "TFLOP/s": round(tf, 1),
+                     "mfma_frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 4), "copies": copies, "steps": steps,
+                     "reps": reps})
+        del gs_, g
+        del Ws, W0, X, Y
+        torch.cuda.empty_cache()
+    return {"what": f"torch {torch.__version__} bf16 matmul (hipBLASLt), dense weights, same graph + events method",
+            "rows": rows}
 
 
-def _copies_for(nbytes, min_copies=2, working_set=600 << 20, cap=16):
-    """Enough rotated weight copies that the working set exceeds the 256 MB
-    Infinity Cache (bounded by `cap`)."""
-    return int(max(min_copies, min(cap, -(-working_set // max(nbytes, 1)))))
-
-
-def bench_configs(dev, lib, args, rng):
-    """The remaining configurations of the measurement table: cfg1, cfg2b
-    (decode), cfg3b/3c (prefill), cfg4 (small M through the routed op, all
-    three quantizations), cfg5 (routed experts).  Same timing method as the
-    headline: rotated weight copies, one graph replay between HIP events.
-    Every configuration is also checked against the oracle (copy 0, one
-    eager call) unless --no-parity."""
+def bench_configs(h, lib, args, rng, ceil):
+    """The remaining configurations of the measurement table, each checked
+    against the oracle (copy 0, one eager call) unless --no-parity, timed by
+    the same method, with the single-launch read ceiling of the same bytes."""
     from cider_press_amd.kernels import gather as kg
     from cider_press_amd.kernels import qmm as kqmm
     from cider_press_amd.kernels import qmv as kqmv
@@ -254,173 +462,171 @@ def bench_configs(dev, lib, args, rng):
     if not args.no_parity:
         from oracle import oracle as O  # checker only
 
-    steps = args.config_steps
+    steps, warm = args.config_steps, args.warmup
     res = {}
 
-    def eager(fn):
-        cmds = dev.commands()
-        fn(cmds)
-        cmds.commit_and_wait()
+    def hbm(nb, us):
+        gbs = nb / (us * 1e-6) / 1e9
+        return round(gbs, 1), round(gbs / HBM_PEAK_GBS, 4)
 
-    def qmv_case(name, n, k, dtype, bias_noise=0.0):
+    def with_ceiling(row, rot, x_buf, nb, regions=None):
+        c = ceil.measure(regions or _wsb_regions(rot, x_buf), max(10, steps // 2), warm,
+                         grids=(512, 1024, 2048, 4096))
+        row["ceiling_us"] = c["us"]
+        row["ceiling_GB/s"] = round(nb / (c["us"] * 1e-6) / 1e9, 1)
+        row["frac_of_ceiling"] = round(c["us"] / row["us"], 4)
+        return row
+
+    def qmv_case(name, n, k, dtype, bias_noise=0.0, x_len=None, routed=False):
         gs, bits = 64, 4
-        wb = n * k // 2 + 4 * n * (k // gs)
-        cps, h0 = _weights(dev, rng, _copies_for(wb), n, k, gs, bits, dtype, bias_noise)
-        x = make_x(rng, 1, k, dtype)
-        X = dev.upload(x.reshape(-1), dtype)
-        Y = dev.alloc_buffer(n, dtype)
-        par = None
-        if O is not None:
-            eager(lambda c: kqmv.affine_qmv(c, lib, *cps[0], X, Y, k, gs, bits))
-            ref = O.qmm_ref(x, *h0, 1, n, k, gs, bits, dtype, threads=ORACLE_THREADS)
-            par = parity_entry(O.tolerance_report(Y.to_numpy().reshape(1, n), ref, x, k, dtype))
-        ms = time_graph(dev, steps, args.warmup,
-                        lambda c, i: kqmv.affine_qmv(c, lib, *cps[i % len(cps)], X, Y, k, gs, bits))
-        nb = algo_bytes(1, n, k, gs, bits)
-        res[name] = {"shape": f"x[1,{k}] . W[{n},{k}]^T 4b gs64 {dtype}", "us": round(ms * 1e3, 2),
-                     "GB/s": round(nb / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                     "copies": len(cps), "parity": par}
+        rot = Rotation(h.dev, rng, n, k, gs, bits, dtype, bias_noise)
+        xl = x_len or k
+        x = make_x(rng, 1, xl, dtype)
+        X = h.dev.upload(x.reshape(-1), dtype)
+        Y = h.dev.alloc_buffer(n, dtype)
 
-    def qmm_case(name, m, n, k):
-        gs, bits, dtype = 64, 4, "bf16"
-        wb = n * k // 2 + 4 * n * (k // gs)
-        cps, h0 = _weights(dev, rng, _copies_for(wb), n, k, gs, bits, dtype)
-        x = make_x(rng, m, k, dtype)
-        X = dev.upload(x.reshape(-1), dtype)
-        Y = dev.alloc_buffer(m * n, dtype)
+        def call(c, i):
+            kqmv.affine_qmv(c, lib, *rot[i], X, Y, k, gs, bits)
+
         par = None
         if O is not None:
-            eager(lambda c: kqmm.affine_qmm_t(c, lib, *cps[0], X, Y, m, n, k, gs, bits))
+            h.eager(lambda c: call(c, 0))
+            xk = np.zeros((1, k), np.uint16)
+            xk[:, :xl] = x
+            ref = O.qmm_ref(xk, *rot.host0, 1, n, k, gs, bits, dtype, threads=ORACLE_THREADS)
+            par = parity_entry(O.tolerance_report(Y.to_numpy().reshape(1, n), ref, xk, k, dtype))
+        t = h.time(call, steps, warm)
+        nb = algo_bytes(1, n, k, gs, bits)
+        gbs, frac = hbm(nb, t["us"])
+        row = {"shape": f"x[1,{xl}] . W[{n},{k}]^T 4b gs64 {dtype}", **_timing(t), "GB/s": gbs, "hbm_frac": frac,
+               "copies": rot.n_copies, "working_set_MB": rot.working_set_mb, "parity": par}
+        return with_ceiling(row, rot, X, nb)
+
+    def qmm_case(name, m, n, k, bits=4, gs=64, routed=False):
+        dtype = "bf16"
+        rot = Rotation(h.dev, rng, n, k, gs, bits, dtype)
+        x = make_x(rng, m, k, dtype)
+        X = h.dev.upload(x.reshape(-1), dtype)
+        Y = h.dev.alloc_buffer(m * n, dtype)
+
+        def call(c, i):
+            if routed:
+                kqmm.quantized_matmul(c, *rot[i], X, Y, m, n, k, gs, bits)
+            else:
+                kqmm.affine_qmm_t(c, lib, *rot[i], X, Y, m, n, k, gs, bits)
+
+        par = None
+        if O is not None:
+            h.eager(lambda c: call(c, 0))
             rows = check_rows(m)
             y = Y.to_numpy().reshape(m, n)
-            ref = O.qmm_ref(x[rows], *h0, len(rows), n, k, gs, bits, dtype, threads=ORACLE_THREADS)
+            ref = O.qmm_ref(x[rows], *rot.host0, len(rows), n, k, gs, bits, dtype, threads=ORACLE_THREADS)
             par = parity_entry(O.tolerance_report(y[rows], ref, x[rows], k, dtype), rows=len(rows))
             par["all_finite"] = bool(np.all(np.isfinite(O.bits_to_f32(y, dtype))))
-        ms = time_graph(dev, max(10, steps // 4), args.warmup,
-                        lambda c, i: kqmm.affine_qmm_t(c, lib, *cps[i % len(cps)], X, Y, m, n, k, gs, bits))
-        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-        res[name] = {"shape": f"X[{m},{k}] . W[{n},{k}]^T 4b gs64 bf16", "us": round(ms * 1e3, 2),
-                     "TFLOP/s": round(tf, 1), "mfma_frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 4), "copies": len(cps),
-                     "parity": par}
+        t = h.time(call, steps if m <= 64 else max(10, steps // 4), warm)
+        nb = algo_bytes(m, n, k, gs, bits)
+        tf = 2.0 * m * n * k / (t["us"] * 1e-6) / 1e12
+        gbs, frac = hbm(nb, t["us"])
+        row = {"shape": f"X[{m},{k}] . W[{n},{k}]^T {bits}b gs{gs} bf16", **_timing(t), "TFLOP/s": round(tf, 2),
+               "mfma_frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 4), "GB/s": gbs, "hbm_frac": frac,
+               "copies": rot.n_copies, "working_set_MB": rot.working_set_mb, "parity": par}
+        return row, rot, X, nb
 
-    qmv_case("cfg1", 2048, 2048, "f16", bias_noise=1e-3)
-    qmv_case("cfg2b", 4096, 12288, "bf16")
-    qmm_case("cfg3b", 512, 12288, 4096)
-    qmm_case("cfg3c_n4096", 2048, 4096, 4096)
-    qmm_case("cfg3c_n12288", 2048, 12288, 4096)
+    res["cfg1"] = qmv_case("cfg1", 2048, 2048, "f16", bias_noise=1e-3)
+    res["cfg2b"] = qmv_case("cfg2b", 4096, 12288, "bf16")
+    for name, m, n, k, bits in (("cfg3b", 512, 12288, 4096, 4), ("cfg3c_n4096", 2048, 4096, 4096, 4),
+                                ("cfg3c_n12288", 2048, 12288, 4096, 4), ("qmm_8bit_m512", 512, 4096, 4096, 8)):
+        row, _, _, _ = qmm_case(name, m, n, k, bits=bits)
+        res[name] = row
 
     # cfg4: small M through the routed op (eval.rs routing), K = N = 4096.
     rows = []
     n = k = 4096
     for bits, gs in ((4, 64), (4, 32), (8, 64)):
-        wb = n * k * bits // 8 + 4 * n * (k // gs)
-        cps, h0 = _weights(dev, rng, _copies_for(wb), n, k, gs, bits, "bf16")
         for m in (1, 4, 16, 64):
-            x = make_x(rng, m, k, "bf16")
-            X = dev.upload(x.reshape(-1), "bf16")
-            Y = dev.alloc_buffer(m * n, "bf16")
-            par = None
-            if O is not None:
-                eager(lambda c: kqmm.quantized_matmul(c, *cps[0], X, Y, m, n, k, gs, bits))
-                ref = O.qmm_ref(x, *h0, m, n, k, gs, bits, "bf16", threads=ORACLE_THREADS)
-                par = parity_entry(O.tolerance_report(Y.to_numpy().reshape(m, n), ref, x, k, "bf16"))
-            ms = time_graph(dev, steps, args.warmup,
-                            lambda c, i: kqmm.quantized_matmul(c, *cps[i % len(cps)], X, Y, m, n, k, gs, bits))
-            nb = algo_bytes(m, n, k, gs, bits)
-            tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-            rows.append({"bits": bits, "gs": gs, "m": m, "us": round(ms * 1e3, 2),
-                         "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
-                         "hbm_frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                         "TFLOP/s": round(tf, 2), "mfma_frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 5),
-                         "kernel": "qmv" if m == 1 else ("small-M" if m <= (64 if n <= 8192 else 32) else "prefill"),
-                         "parity": par})
-        del cps
+            row, rot, X, nb = qmm_case(f"cfg4_{bits}b_gs{gs}_m{m}", m, n, k, bits=bits, gs=gs, routed=True)
+            row = {"bits": bits, "gs": gs, "m": m, **row}
+            rows.append(with_ceiling(row, rot, X, nb))
+            del rot
     res["cfg4"] = rows
 
     # cfg5: 128 experts, W_up [768, 2048] and W_down [2048, 768], 4b gs64;
-    # 256 tokens routed top-8 (uniform, without replacement) -> 2048 rows.
-    e, tokens, topk = 128, 256, 8
-    route = make_routing(rng, tokens, topk, e).reshape(-1)
-    lhs = np.repeat(np.arange(tokens, dtype=np.uint32), topk)
-    order = np.argsort(route, kind="stable")
+    # 256 tokens routed top-8 (uniform, without replacement) -> 2048 rows;
+    # decode-shaped routing: 1 and 4 tokens x top-8.
+    e, topk = 128, 8
     for proj, (n, k) in (("up", (768, 2048)), ("down", (2048, 768))):
         gs, bits = 64, 4
-        wb = e * (n * k // 2 + 4 * n * (k // gs))
-        cps, h0 = _weights(dev, rng, _copies_for(wb, cap=6), e * n, k, gs, bits, "bf16")
-        xin = make_x(rng, tokens if proj == "up" else tokens * topk, k, "bf16")
-        X = dev.upload(xin.reshape(-1), "bf16")
-        nrows = tokens * topk
-        Y = dev.alloc_buffer(nrows * n, "bf16")
-        for label, sorted_rows in (("unsorted", False), ("sorted", True)):
-            rhs = (route[order] if sorted_rows else route).astype(np.uint32)
-            lh = lhs[order] if sorted_rows else lhs
-            if proj == "down":
-                lh = None  # row r of the down projection reads its own hidden row
-            R = dev.upload(rhs, "u32")
-            L = dev.upload(lh.astype(np.uint32), "u32") if lh is not None else None
+        rot = Rotation(h.dev, rng, e * n, k, gs, bits, "bf16")
+        per_w, per_s = n * k // 8, n * (k // gs)
+        for tokens in (256, 4, 1):
+            route = make_routing(rng, tokens, topk, e).reshape(-1)
+            lhs = np.repeat(np.arange(tokens, dtype=np.uint32), topk)
+            order = np.argsort(route, kind="stable")
+            xin = make_x(rng, tokens if proj == "up" else tokens * topk, k, "bf16")
+            X = h.dev.upload(xin.reshape(-1), "bf16")
+            nrows = tokens * topk
+            Y = h.dev.alloc_buffer(nrows * n, "bf16")
+            labels = (("unsorted", False), ("sorted", True)) if tokens == 256 else (("sorted", True),)
+            for label, sorted_rows in labels:
+                rhs = (route[order] if sorted_rows else route).astype(np.uint32)
+                lh = lhs[order] if sorted_rows else lhs
+                if proj == "down":
+                    lh = None  # row r of the down projection reads its own hidden row
+                R = h.dev.upload(rhs, "u32")
+                Lb = h.dev.upload(lh.astype(np.uint32), "u32") if lh is not None else None
 
-            def call(c, ws, L=L, R=R, sorted_rows=sorted_rows):
-                kg.affine_gather_qmm(c, lib, X, *ws, L, R, Y, nrows, n, k, e, gs, bits,
-                                     sorted_indices=sorted_rows, x_rows=xin.shape[0])
+                def call(c, i, Lb=Lb, R=R, sorted_rows=sorted_rows, X=X, Y=Y, nrows=nrows, xin=xin):
+                    kg.affine_gather_qmm(c, lib, X, *rot[i], Lb, R, Y, nrows, n, k, e, gs, bits,
+                                         sorted_indices=sorted_rows, x_rows=xin.shape[0])
 
-            par = None
-            if O is not None:
-                eager(lambda c: call(c, cps[0]))
-                ref = O.gather_qmm_ref(xin, lh, rhs, *h0, nrows, n, k, gs, bits, "bf16", threads=ORACLE_THREADS)
-                par = parity_entry(O.tolerance_report(Y.to_numpy().reshape(nrows, n), ref, xin, k, "bf16"))
-            ms = time_graph(dev, max(10, steps // 2), args.warmup, lambda c, i: call(c, cps[i % len(cps)]))
-            touched = len(np.unique(rhs))
-            nb = touched * (n * k // 2 + 4 * n * (k // gs)) + nrows * k * 2 + nrows * n * 2
-            tf = 2.0 * nrows * n * k / (ms * 1e-3) / 1e12
-            res[f"cfg5_{proj}_{label}"] = {
-                "shape": f"{nrows} rows x {e} experts W[{n},{k}] 4b gs64 bf16", "us": round(ms * 1e3, 2),
-                "GB/s": round(nb / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                "TFLOP/s": round(tf, 2), "experts_touched": touched, "copies": len(cps), "parity": par}
-        del cps
+                par = None
+                if O is not None:
+                    h.eager(lambda c: call(c, 0))
+                    ref = O.gather_qmm_ref(xin, lh, rhs, *rot.host0, nrows, n, k, gs, bits, "bf16",
+                                           threads=ORACLE_THREADS)
+                    par = parity_entry(O.tolerance_report(Y.to_numpy().reshape(nrows, n), ref, xin, k, "bf16"))
+                t = h.time(call, max(10, steps // 2), warm)
+                touched = len(np.unique(rhs))
+                nb = touched * (n * k // 2 + 4 * n * (k // gs)) + nrows * k * 2 + nrows * n * 2
+                tf = 2.0 * nrows * n * k / (t["us"] * 1e-6) / 1e12
+                gbs, frac = hbm(nb, t["us"])
+                key = f"cfg5_{proj}_{label}" if tokens == 256 else f"cfg5_decode_t{tokens}_{proj}"
+                row = {"shape": f"{tokens} tokens x top-{topk} -> {nrows} rows, {e} experts W[{n},{k}] 4b gs64 bf16",
+                       **_timing(t), "GB/s": gbs, "hbm_frac": frac, "TFLOP/s": round(tf, 2),
+                       "experts_touched": touched, "copies": rot.n_copies, "working_set_MB": rot.working_set_mb,
+                       "parity": par}
+                # Ceiling: a plain read of the same byte count (touched experts'
+                # tables, contiguous) plus the activation rows.
+                regs = [[(W.ptr, touched * per_w * 4), (S.ptr, touched * per_s * 2), (B.ptr, touched * per_s * 2),
+                         (X.ptr, X.byte_len)] for W, S, B in rot.copies]
+                res[key] = with_ceiling(row, rot, X, nb, regions=regs)
+        del rot
+
+    # The reference's own benchmark shapes (Qwen2.5-0.5B): decode qmv with its
+    # published M4 Max figures beside ours, and M = 39 prefill.
+    ref_rows = []
+    for k, n, label, xl, pub in REF_QMV_SHAPES:
+        row = qmv_case(label, n, k, "bf16", x_len=xl)
+        ref_rows.append({"label": label, **row, "reference_M4_Max_GB/s": pub,
+                         "ratio_to_reference": round(row["GB/s"] / pub, 2)})
+    res["reference_qmv_qwen2.5_0.5b"] = ref_rows
+    ref_rows = []
+    for k, n, label in REF_QMM_SHAPES:
+        row, rot, X, nb = qmm_case(label, REF_QMM_M, n, k)
+        ref_rows.append(with_ceiling({"label": label, **row}, rot, X, nb))
+        del rot
+    res["reference_qmm_m39_qwen2.5_0.5b"] = ref_rows
     return res
 
 
-def bench_ceiling(dev, args, rng, q=None):
-    """HBM ceiling of one launch over the qmv config 2a bytes: a plain
-    streaming read (cpq_stream_read) of the same kind of rotated copies
-    (W, scales, biases, x), timed by the same graph method as the decode
-    kernel.  Two grid sizes; the faster one is the ceiling."""
-    import ctypes
-
-    from cider_press_amd import _lib
-
-    n, k, gs, bits, dtype = 12288, 4096, 64, 4, "bf16"
-    if q is not None and q.get("copies"):
-        copies, X = q["copies"], q["X"]
-    else:
-        copies, _ = make_copies(dev, rng, args.copies, n, k, gs, bits, dtype)
-        from cider_press_amd.synthetic import make_x
-
-        X = dev.upload(make_x(rng, 1, k, dtype).reshape(-1), dtype)
-    sink = dev.alloc_buffer(1, "u32")
-    L = _lib.lib()
-    regs = []
-    for W, S, B in copies:
-        ptrs = (ctypes.c_void_p * 4)(W.ptr, S.ptr, B.ptr, X.ptr)
-        lens = (ctypes.c_size_t * 4)(W.byte_len, S.byte_len, B.byte_len, X.byte_len)
-        regs.append((ptrs, lens))
-    nbytes = sum(int(v) for v in regs[0][1])
-    out = {"what": "plain streaming read of the same rotated copies (W, scales, biases, x) in one launch per "
-                   "step, same graph method as the decode kernel", "bytes_read": nbytes, "grids": {}}
-    best = None
-    for nwg in (768, 2048):
-        def step(c, i, nwg=nwg):
-            ptrs, lens = regs[i % len(regs)]
-            _lib.check(L.cpq_stream_read(c.handle, ptrs, lens, 4, ctypes.c_void_p(sink.ptr), nwg))
-
-        ms = time_graph(dev, args.steps, args.warmup, step)
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        out["grids"][str(nwg)] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1)}
-        if best is None or gbs > best:
-            best = gbs
-    out["GB/s"] = round(best, 1)
-    out["frac_of_peak"] = round(best / HBM_PEAK_GBS, 4)
-    return out
+def launch_floor(h, args):
+    """Per-step time of a graph of one-workgroup, 16-byte reads: the launch
+    cost any kernel here pays."""
+    buf = h.dev.alloc_buffer(4, "u32")
+    ptrs = (ctypes.c_void_p * 1)(buf.ptr)
+    lens = (ctypes.c_size_t * 1)(16)
+    t = h.time(lambda c, i: h.stream_read(c, ptrs, lens, 1, 1, 0), args.steps, args.warmup)
+    return {"what": "one workgroup reading 16 bytes per step, same graph method", **_timing(t)}
 
 
 def _cpu_model():
@@ -435,16 +641,17 @@ def _cpu_model():
 
 
 def cpu_baseline(q, budget_s):
-    """Oracle dequantize-and-dot (T-rounded weights, fp32 accumulate) on the
-    host: all-core and single-thread qmv GB/s at config 2a, and config 3a
-    GFLOP/s on a row sample.  Uses the AVX-512 build where the host has it."""
+    """Host dequantize-and-dot (T-rounded weights, fp32 accumulate), each form
+    of oracle/cpu_baseline.c that the host runs (scalar, AVX2, AVX-512): qmv
+    config 2a GB/s on all cores and one core, and config 3a GFLOP/s on a row
+    sample.  `value` is the fastest all-core form."""
     from oracle import oracle as O
     from cider_press_amd.synthetic import make_x
 
     n, k, gs, bits = q["shape"]
     w, s, b = q["host0"]
     threads = min(16, os.cpu_count() or 1)
-    isa = O.baseline_isa()
+    forms = O.baseline_forms()
 
     def timed(fn, seconds):
         fn()  # warm-up
@@ -455,25 +662,27 @@ def cpu_baseline(q, budget_s):
             times.append(time.perf_counter() - t1)
         return float(np.median(times)), len(times)
 
-    all_s, all_n = timed(lambda: O.cpu_baseline(q["x"], w, s, b, 1, n, k, gs, bits, "bf16", threads=threads),
-                         budget_s * 0.5)
-    one_s, one_n = timed(lambda: O.cpu_baseline(q["x"], w, s, b, 1, n, k, gs, bits, "bf16", threads=1),
-                         budget_s * 0.25)
-    # cfg3a (M=512, N=K=4096) on a sample of 32 activation rows x all 4096
-    # output rows of copy 0's first 4096 rows: 2*32*4096*4096 FLOP per call.
+    per_form = {}
+    share = budget_s / max(1, len(forms))
     mq, nq = 32, 4096
     xq = make_x(np.random.default_rng(1), mq, k, "bf16")
     wq, sq, bq = w[:nq], s[:nq], b[:nq]
-    qmm_s, qmm_n = timed(lambda: O.cpu_baseline(xq, wq, sq, bq, mq, nq, k, gs, bits, "bf16", threads=threads),
-                         budget_s * 0.25)
-    return {"value": round(q["bytes"] / all_s / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"qmv config 2a (N=12288, K=4096, 4-bit gs64, bf16), median of {all_n} calls "
-                      f"over {budget_s * 0.5:.0f} s, {threads} threads, oracle C dequantize-and-dot ({isa})",
-            "nproc": os.cpu_count(), "cpu_model": _cpu_model(), "isa": isa,
-            "single_thread_GB/s": round(q["bytes"] / one_s / 1e9, 3), "single_thread_calls": one_n,
-            "qmm_cfg3a_GFLOP/s": round(2.0 * mq * nq * k / qmm_s / 1e9, 2),
-            "qmm_sample": f"config 3a shape on {mq} of its 512 activation rows (K=N=4096), median of {qmm_n} calls, "
-                          f"{threads} threads"}
+    for form in forms:
+        all_s, all_n = timed(lambda: O.cpu_baseline(q["x"], w, s, b, 1, n, k, gs, bits, "bf16", threads=threads,
+                                                    form=form), share * 0.45)
+        one_s, one_n = timed(lambda: O.cpu_baseline(q["x"], w, s, b, 1, n, k, gs, bits, "bf16", threads=1,
+                                                    form=form), share * 0.3)
+        qmm_s, qmm_n = timed(lambda: O.cpu_baseline(xq, wq, sq, bq, mq, nq, k, gs, bits, "bf16", threads=threads,
+                                                    form=form), share * 0.25)
+        per_form[form] = {"GB/s": round(q["bytes"] / all_s / 1e9, 3), "calls": all_n,
+                          "single_thread_GB/s": round(q["bytes"] / one_s / 1e9, 3), "single_thread_calls": one_n,
+                          "qmm_cfg3a_GFLOP/s": round(2.0 * mq * nq * k / qmm_s / 1e9, 2), "qmm_calls": qmm_n}
+    best = max(per_form, key=lambda f: per_form[f]["GB/s"])
+    return {"value": per_form[best]["GB/s"], "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"qmv config 2a (N=12288, K=4096, 4-bit gs64, bf16), median over about "
+                      f"{share * 0.45:.0f} s of calls, {threads} threads, {best} form of the C dequantize-and-dot "
+                      f"(oracle/cpu_baseline.c); config 3a sampled on {mq} of its 512 activation rows",
+            "form": best, "forms": per_form, "nproc": os.cpu_count(), "cpu_model": _cpu_model()}
 
 
 def bench_copy(args):
@@ -609,13 +818,14 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--qmm-steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--copies", type=int, default=16)
-    ap.add_argument("--only", choices=["qmv", "qmm", "all", "copy", "configs", "ceiling"], default="all")
-    ap.add_argument("--no-configs", action="store_true", help="skip the cfg1/2b/3b/3c/4/5 table")
+    ap.add_argument("--only", choices=["qmv", "qmm", "all", "copy", "configs", "ceiling", "dense"], default="all")
+    ap.add_argument("--no-configs", action="store_true", help="skip the configs table")
+    ap.add_argument("--no-dense", action="store_true", help="skip the dense bf16 GEMM anchor")
+    ap.add_argument("--no-graph", action="store_true", help="encode timed calls directly (no graph capture)")
     ap.add_argument("--config-steps", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"))
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_DIR")
     ap.add_argument("--counter-summary", nargs="+", metavar="PMC_DIR")
@@ -624,11 +834,9 @@ def main():
     if args.counter_summary:
         counter_summary(args.counter_summary)
         return
-
     if args.trace_summary:
         trace_summary(args.trace_summary)
         return
-
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
         return
@@ -638,58 +846,91 @@ def main():
                                    "(the quantized-matmul path is measured on a single MI355X)"}))
         sys.exit(2)
 
-    from cider_press_amd.kernels import Device, KernelLibrary
-
     if args.only == "copy":
         print(json.dumps(bench_copy(args)), flush=True)
         return
+    if args.only == "dense":
+        print(json.dumps(bench_dense(args)), flush=True)
+        return
+
+    # The dense anchor runs in a child process started before this process
+    # touches the GPU: torch's ROCm build carries its own HIP runtime, which
+    # does not see the device once the system runtime libcpq.so links has
+    # opened it in the same process.
+    dense = None
+    if args.only == "all" and not args.no_dense:
+        import subprocess
+
+        cmd = [sys.executable, os.path.abspath(__file__), "--only", "dense", "--qmm-steps", str(args.qmm_steps)]
+        # Run to completion first: the two processes must not share the GPU
+        # while either one times.
+        dense = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+
+    from cider_press_amd.kernels import Device, KernelLibrary
 
     dev = Device.system_default()
     lib = KernelLibrary.quantized(dev)
     info = dev.info()
     rng = np.random.default_rng(0)
+    h = Harness(dev, use_graph=not args.no_graph)
+    ceil = Ceiling(h)
 
     line = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded uniform nibbles, U(0.002,0.02) "
             "scales, biases=-8*scale, x~N(0,1))",
-            "config": {"workload": "qmv config 2a: x[1,4096] . W[12288,4096]^T, 4-bit gs64, bf16, "
-                                   f"{args.copies} rotated weight copies", "device": info["name"],
-                       "cu_count": info["cu_count"]}}
+            "config": {"workload": "qmv config 2a: x[1,4096] . W[12288,4096]^T, 4-bit gs64, bf16",
+                       "device": info["name"], "cu_count": info["cu_count"],
+                       "timing": "median of timed graph replays, each behind a 512 MiB read, no host sync between"
+                                 if h.use_graph else "eager launches between events (no graph)"}}
     q = None
-    if args.only == "ceiling":
-        print(json.dumps(bench_ceiling(dev, args, rng)), flush=True)
-        return
-    if args.only in ("qmv", "all"):
-        q = bench_qmv(dev, lib, args, rng)
+    if args.only in ("qmv", "all", "ceiling"):
+        q = bench_qmv(h, lib, args, rng, ceil)
         line["value"] = round(q["gbs"], 2)
-        line["ms_per_step"] = q["ms"]
+        line["ms_per_step"] = q["t"]["us"] * 1e-3
+        line["config"]["copies"] = q["copies"]
+        line["config"]["working_set_MB"] = q["working_set_mb"]
+        line["timing"] = _timing(q["t"])
         line["roofline"] = {"bound": "hbm", "achieved": round(q["gbs"], 2), "peak": HBM_PEAK_GBS,
                             "unit": "GB/s", "frac": round(q["gbs"] / HBM_PEAK_GBS, 4),
                             "traffic": load_traffic("qmv", QMV_KERNEL)}
         line["parity"] = {"qmv": q["parity"]}
-        c = bench_ceiling(dev, args, rng, q)
-        c["qmv_frac_of_ceiling"] = round(q["gbs"] / c["GB/s"], 4)
-        line["ceiling"] = c
+        line["ceiling"] = q["ceiling"]
+        line["launch_floor"] = launch_floor(h, args)
+        if args.only == "ceiling":
+            print(json.dumps(line), flush=True)
+            return
     if args.only in ("qmm", "all"):
-        r = bench_qmm(dev, lib, args, rng)
+        r = bench_qmm(h, lib, args, rng)
         line["qmm"] = {"workload": "config 3a: X[512,4096] . W[4096,4096]^T, 4-bit gs64, bf16",
                        "value": round(r["tflops"], 2), "unit": "TFLOP/s", "steps": args.qmm_steps,
-                       "ms_per_step": r["ms"],
+                       "ms_per_step": r["t"]["us"] * 1e-3, "timing": _timing(r["t"]), "copies": r["copies"],
+                       "working_set_MB": r["working_set_mb"],
                        "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2),
                                     "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                                     "frac": round(r["tflops"] / BF16_MFMA_PEAK_TFLOPS, 4),
                                     "traffic": load_traffic("qmm", QMM_KERNEL)}}
         line.setdefault("parity", {})["qmm"] = r["parity"]
         if args.only == "qmm":
-            line["metric"] = METRIC
             line["value"] = round(r["tflops"], 2)
             line["unit"] = "TFLOP/s"
-            line["ms_per_step"] = r["ms"]
+            line["ms_per_step"] = r["t"]["us"] * 1e-3
             line["steps"] = args.qmm_steps
             line["roofline"] = line["qmm"]["roofline"]
+    if dense is not None:
+        out, err = dense.stdout, dense.stderr
+        js = [ln for ln in out.splitlines() if ln.startswith("{")]
+        if dense.returncode == 0 and js:
+            d = json.loads(js[-1])
+            line["dense_anchor"] = d
+            if "qmm" in line:
+                d0 = d["rows"][0]
+                line["qmm"]["dense_anchor_TFLOP/s"] = d0["TFLOP/s"]
+                line["qmm"]["vs_dense_anchor"] = round(line["qmm"]["value"] / d0["TFLOP/s"], 3)
+        else:  # the anchor is optional measurement
+            line["dense_anchor"] = {"error": f"rc={dense.returncode}: {err[-400:]}"}
     if (args.only == "all" and not args.no_configs) or args.only == "configs":
-        line["configs"] = bench_configs(dev, lib, args, rng)
+        line["configs"] = bench_configs(h, lib, args, rng, ceil)
     if q is not None and not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(q, args.cpu_seconds)
     print(json.dumps(line), flush=True)

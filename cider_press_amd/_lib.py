@@ -152,6 +152,8 @@ SIGNATURES = {
     "cpq_event_elapsed_ms": (_st, [_vp, _vp, _c.POINTER(_c.c_float)]),
     "cpq_event_release": (None, [_vp]),
     "cpq_stream_read": (_st, [_vp, _c.POINTER(_vp), _c.POINTER(_sz), _int, _vp, _int]),
+    "cpq_stream_read_variant": (_st, [_vp, _c.POINTER(_vp), _c.POINTER(_sz), _int, _vp, _int, _int]),
+    "cpq_stream_read_variant_count": (_int, []),
     "cpq_quantization_validate": (_st, [_u32, _u32]),
     "cpq_packed_word_count": (_st, [_u32, _u32, _sz, _psz]),
     "cpq_group_count": (_st, [_u32, _u32, _sz, _psz]),

@@ -175,6 +175,21 @@ hipError_t launch_qmm(hipStream_t s, const QmmPlan& plan, void* scratch, const Q
 // qmm_plan + launch_qmm on a session (its stream, CU count and scratch).
 hipError_t launch_session_qmm(cpq_commands* cmds, const QuantArgs& q, const void* x, void* y, int m, int n, int k);
 
+// Where a matmul runs: stream, CU count, the split-K scratch at hand and the
+// capacity plans are made for (plans needing more than scratch_bytes are
+// remade for scratch_bytes).
+struct ExecCtx {
+  hipStream_t stream;
+  int cu_count;
+  void* scratch;
+  size_t plan_bytes;
+  size_t scratch_bytes;
+};
+ExecCtx session_ctx(const cpq_commands* cmds);
+// Y = X . W^T with the kernel chosen by M (small-M kernels, else the prefill
+// plan), as affine_qmm_t and the runtime node run it.
+hipError_t launch_matmul(const ExecCtx& ex, const QuantArgs& q, const void* x, void* y, int m, int n, int k);
+
 // Capacity of a session's scratch when CPQ_SESSION_SCRATCH_MB is not set.
 constexpr size_t kDefaultSessionScratchBytes = size_t(64) << 20;
 
@@ -218,6 +233,16 @@ hipError_t launch_gather_expert(hipStream_t s, const QuantArgs& q, const void* x
                                 int n_experts, int n, int k, bool sorted, int cu_count,
                                 unsigned int* status);
 
+// Routed experts at decode shapes (kernels/gather_decode.hip): up to 64
+// rows, 4/8-bit, K % 128 == 0; one workgroup per (distinct expert, 16
+// columns); validates the indices itself.
+int gather_decode_kw(int n_rows, int n, int k);
+size_t gather_decode_lds(int n_rows, int k, int kw);
+bool gather_decode_supported(const QuantArgs& q, int n_rows, int n, int k);
+hipError_t launch_gather_decode(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
+                                const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
+                                unsigned int* status);
+
 // Whether some routed-expert kernel takes this shape: the expert-major
 // kernel, or the per-slab kernel while its slab constants fit in LDS.
 bool gather_supported(int bits, int n_rows, int n, int k, int gs);
@@ -250,9 +275,11 @@ hipError_t launch_qmm_small(hipStream_t s, const SmallPlan& p, void* scratch, co
 // Row-count threshold below which cpq_quantized_matmul uses the skinny kernel.
 int skinny_max_m(const QuantArgs& q, int n, int k);
 
-// Plain streaming read of up to 4 regions (measurement support).
+// Plain streaming read of up to 4 regions (measurement support), in one of
+// stream_read_variant_count() designs.
 hipError_t launch_stream_read(hipStream_t s, const void* const* regions, const size_t* bytes, int n_regions,
-                              uint32_t* sink, int n_wg);
+                              uint32_t* sink, int n_wg, int variant);
+int stream_read_variant_count();
 
 // Integer from the environment (tuning and test hooks), dflt when unset.
 inline int env_int(const char* name, int dflt) {

@@ -1,0 +1,334 @@
+// Routed experts at decode shapes: a few (token, expert) rows, each against
+// its own expert's weight matrix.
+//
+// Reference op: the rhs-indexed gather of MLX, affine_gather_qmv_fast /
+// affine_gather_qmv (kernels-mlx/mlx/backend/metal/kernels/quantized.h:
+// 1905-2028), which runs one GEMV per (row, expert).  Numerics as every path
+// here: each weight is dequantized to T (RNE of fmaf(s, q, b)), products
+// accumulate in fp32 on the matrix cores, the output is rounded to T once.
+//
+// HBM-bound.  Rows that pick the same expert share one pass over its
+// weights, so the bytes read are those of the distinct experts touched.
+//   - Workgroup (column block cb, slot u): 16 output columns of the u-th
+//     distinct expert of the call (distinct experts numbered by the first row
+//     that names them).  Every wave reads all of rhs (n_rows <= 64: one load
+//     per lane) and derives the slot's expert and its rows with ballots, so no
+//     sort or pre-pass kernel runs; slots past the number of distinct experts
+//     exit at once, except the first of them, which zeroes this column block
+//     of rows whose expert index is out of range.
+//   - The slot's rows go through the matrix cores kDecPass at a time (a
+//     slot at decode holds one or two rows; a small pass keeps the LDS per
+//     workgroup small, so several workgroups share a CU): MFMA
+//     16x16x32 with A = the rows' activations (staged in LDS) and B = 8
+//     dequantized weights per lane, lane (r, g) holding column n0 + r and
+//     chunk 4j + g of step j (128 k per step), as in the decode kernel.
+//   - The 4 waves of a workgroup split K into KW contiguous step ranges and
+//     the columns into 4 / KW blocks of 16 (KW chosen by the grid size, see
+//     gather_decode_kw); each wave issues the weight
+//     and (scale, bias) loads of its range (up to 8 steps) before staging its
+//     own activation slices, votes on the single-FMA dequantization within
+//     the wave, then multiplies.  The K parts are summed through LDS in wave
+//     order.
+//   - Index checks: rows with an out-of-range expert or activation index are
+//     written as zeros and counted into *status (by workgroup (0, 0)),
+//     together with descents of a routing declared sorted; no index is used
+//     to address memory before it is checked.
+#include <algorithm>
+
+#include "../cpq_internal.hpp"
+#include "common.hpp"
+
+namespace cpq {
+namespace {
+
+using namespace dev;
+
+constexpr int kDecPF = 8;       // steps of loads in flight per wave
+constexpr int kDecMaxRows = 64; // rows of one call (one lane each)
+constexpr int kDecPass = 4;     // rows of a slot per pass (decode slots hold one or two)
+constexpr int kDecWaves = 4;    // waves per workgroup: KW split K, 4 / KW column blocks
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+
+template <int BITS>
+__device__ __forceinline__ void dec_load(__amdgpu_buffer_rsrc_t wr, uint32_t voff, uint32_t* dst) {
+  const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff, 0, 0));
+  dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+  if constexpr (BITS == 8) {
+    const u32x4 v1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff + 16, 0, 0));
+    dst[4] = v1.x; dst[5] = v1.y; dst[6] = v1.z; dst[7] = v1.w;
+  }
+}
+
+// Four MFMAs of one step: activation slices from the wave's LDS rows, the
+// lane's chunk dequantized slice by slice.
+template <typename TT, int BITS, bool FAST>
+__device__ __forceinline__ f32x4 dec_step(const uint32_t* wq, uint32_t sv, uint32_t bv, const unsigned char* xrow,
+                                          int m, f32x4 acc) {
+  const float s = TT::to_f32((uint16_t)sv), b = TT::to_f32((uint16_t)bv);
+  const float s16 = s * 0.0625f, c0 = fmaf(-1024.f, s, b), c1 = fmaf(-64.f, s, b);
+  const int g4 = (threadIdx.x >> 4) & 3;
+  const u32x4 a0 = *reinterpret_cast<const u32x4*>(xrow + (((4 * g4 + 0) ^ m) << 4));
+  const u32x4 a1 = *reinterpret_cast<const u32x4*>(xrow + (((4 * g4 + 1) ^ m) << 4));
+  const u32x4 a2 = *reinterpret_cast<const u32x4*>(xrow + (((4 * g4 + 2) ^ m) << 4));
+  const u32x4 a3 = *reinterpret_cast<const u32x4*>(xrow + (((4 * g4 + 3) ^ m) << 4));
+  acc = Mfma16<TT>::run(a0, dequant_slice<TT, BITS, FAST, 0>(wq, s, s16, b, c0, c1), acc);
+  acc = Mfma16<TT>::run(a1, dequant_slice<TT, BITS, FAST, 1>(wq, s, s16, b, c0, c1), acc);
+  acc = Mfma16<TT>::run(a2, dequant_slice<TT, BITS, FAST, 2>(wq, s, s16, b, c0, c1), acc);
+  acc = Mfma16<TT>::run(a3, dequant_slice<TT, BITS, FAST, 3>(wq, s, s16, b, c0, c1), acc);
+  return acc;
+}
+
+template <typename TT, int BITS, int KW>
+__global__ __launch_bounds__(64 * kDecWaves) void gather_decode_kernel(
+    const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    const uint16_t* __restrict__ x, int x_rows, const uint32_t* __restrict__ lhs, const uint32_t* __restrict__ rhs,
+    int n_rows, uint16_t* __restrict__ y, int n_experts, int n, int k, int gs_shift, int sorted, int rows_max,
+    int steps_w, unsigned int* __restrict__ status) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int CB = kDecWaves / KW;  // 16-column blocks per workgroup
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kw = wave % KW, cbl = wave / KW;
+  const int nw0 = blockIdx.x * 16 * CB;  // first column of the workgroup
+  const int n0 = nw0 + 16 * cbl;         // first column of this wave's block
+  const int u = blockIdx.y;
+
+  // 1. Routing: lane i holds row i's expert and activation row.
+  const bool in = lane < n_rows;
+  const uint32_t e = in ? rhs[lane] : 0xffffffffu;
+  const uint32_t xr = in ? (lhs ? lhs[lane] : (uint32_t)lane) : 0u;
+  const bool ev = in && e < (uint32_t)n_experts;
+  const bool lv = in && xr < (uint32_t)x_rows;
+  const uint64_t valid = ballot(ev);
+  uint64_t later = 0;  // rows naming an expert an earlier row already named
+  for (int j = 0; j < n_rows; ++j) {
+    const uint32_t ej = __builtin_amdgcn_readlane(e, j);
+    const uint64_t same = ballot(ev && e == ej);
+    later |= same & (~0ull << j << 1);
+  }
+  const uint64_t first = valid & ~later;
+  const int nuniq = __builtin_popcountll(first);
+  if (blockIdx.x == 0 && u == 0) {
+    const uint32_t nxt = (in && lane + 1 < n_rows) ? rhs[lane + 1] : 0xffffffffu;
+    const int bad = __builtin_popcountll(ballot(in && (!ev || !lv))) +
+                    (sorted ? __builtin_popcountll(ballot(lane + 1 < n_rows && e > nxt)) : 0);
+    if (wave == 0 && lane == 0 && bad) atomicAdd(status, (unsigned)bad);
+  }
+  if (u >= nuniq) {
+    if (u == nuniq) {  // zero this column block of rows with an out-of-range expert
+      const uint64_t badrows = ballot(in && !ev);
+      for (int t = threadIdx.x; t < 64 * 16 * CB; t += 64 * kDecWaves) {
+        const int r = t / (16 * CB), c = nw0 + t % (16 * CB);
+        if (((badrows >> r) & 1) && c < n) y[(size_t)r * n + c] = 0;
+      }
+    }
+    return;
+  }
+  uint64_t fm = first;
+  for (int i = 0; i < u; ++i) fm &= fm - 1;
+  const int lead = __builtin_ctzll(fm);
+  const uint32_t eu = __builtin_amdgcn_readlane(e, lead);
+  const uint64_t rows = ballot(ev && e == eu);
+  const int nr = __builtin_popcountll(rows);
+
+  // 2. This wave's K range and weight stream of expert eu.
+  const int G = k >> gs_shift;
+  const int S = k >> 7;  // steps of 128
+  const int js = (kw * S) / KW, je = ((kw + 1) * S) / KW;
+  const int nst = je - js;
+  const int r = lane & 15, g = lane >> 4;
+  const uint32_t rowbytes = (uint32_t)k * BITS / 8u;
+  const size_t ewords = (size_t)n * (size_t)k * BITS / 32;
+  const size_t egroups = (size_t)n * (size_t)G;
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(w + (size_t)eu * ewords), 0, (int)((uint32_t)n * rowbytes), 0x00020000);
+  const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(scales + (size_t)eu * egroups), 0, (int)((uint32_t)n * (uint32_t)G * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(biases + (size_t)eu * egroups), 0, (int)((uint32_t)n * (uint32_t)G * 2u), 0x00020000);
+  // Columns past N read zeros through the range check (offsets past 2^31,
+  // beyond every range; never stored).
+  const bool col_ok = n0 + r < n;
+  const uint32_t voff0 =
+      col_ok ? (uint32_t)(n0 + r) * rowbytes + (uint32_t)(4 * js + g) * (BITS * 4u) : 0x80000000u;
+  const uint32_t coff0 = col_ok ? (uint32_t)(n0 + r) * (uint32_t)G : 0x40000000u;
+
+  const int RB = min(steps_w, kDecPF) * 256;  // bytes of one activation row in the wave's region
+  unsigned char* xw = smem + (size_t)wave * rows_max * RB;
+  float* red = reinterpret_cast<float*>(smem + (size_t)kDecWaves * rows_max * RB);  // [waves][64][4]
+  int* rlist = reinterpret_cast<int*>(red + kDecWaves * 256);                           // [64]
+
+  // The slot's rows in order: rank -> row.
+  if ((rows >> lane) & 1) rlist[__builtin_popcountll(rows & ((1ull << lane) - 1))] = lane;
+  __syncthreads();
+
+  for (int p0 = 0; p0 < nr; p0 += rows_max) {
+    const int np = min(rows_max, nr - p0);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int b0 = 0; b0 < nst; b0 += kDecPF) {
+      const int nb = min(kDecPF, nst - b0);
+      // 2a. Loads of this batch: weights, then (scale, bias) of each step.
+      uint32_t wq[kDecPF][BITS];
+      uint32_t sv[kDecPF], bv[kDecPF];
+#pragma unroll
+      for (int t = 0; t < kDecPF; ++t)
+        if (t < nb) {
+          dec_load<BITS>(wr, voff0 + (uint32_t)(b0 + t) * (16u * BITS), wq[t]);
+          const uint32_t gi = coff0 + (((uint32_t)(4 * (js + b0 + t) + g) * 32u) >> gs_shift);
+          sv[t] = __builtin_amdgcn_raw_buffer_load_b16(sr, gi * 2u, 0, 0);
+          bv[t] = __builtin_amdgcn_raw_buffer_load_b16(br, gi * 2u, 0, 0);
+        }
+      // 2b. Stage the pass's activation slices of this batch: row m, step t,
+      //     16-byte piece p (natural order) at slot p ^ m of the row's step.
+      const int pieces = np * nb * 16;
+      for (int q = lane; q < pieces; q += 64) {
+        const int m = q / (nb * 16), rem = q - m * (nb * 16), t = rem >> 4, pc = rem & 15;
+        const int row = rlist[p0 + m];
+        const uint32_t xrow = lhs ? lhs[row] : (uint32_t)row;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (xrow < (uint32_t)x_rows)
+          v = *reinterpret_cast<const u32x4*>(x + (size_t)xrow * k + (size_t)(js + b0 + t) * 128 + pc * 8);
+        *reinterpret_cast<u32x4*>(xw + m * RB + t * 256 + ((pc ^ m) << 4)) = interleave_x<BITS>(v);
+      }
+      // 2c. Vote (within the wave) on the single-FMA dequantization.
+      bool ok = true;
+#pragma unroll
+      for (int t = 0; t < kDecPF; ++t)
+        if (t < nb) ok &= fast_ok_bits<TT>(sv[t], bv[t]);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const bool fast = ballot(!ok) == 0;
+      // 2d. Multiply: A row m = lane & 15 (rows past the pass read row np-1:
+      //     their outputs are never stored).
+      const int m = min(r, np - 1);
+      const unsigned char* xrowp = xw + m * RB;
+#pragma unroll
+      for (int t = 0; t < kDecPF; ++t)
+        if (t < nb) {
+          acc = fast ? dec_step<TT, BITS, true>(wq[t], sv[t], bv[t], xrowp + t * 256, m, acc)
+                     : dec_step<TT, BITS, false>(wq[t], sv[t], bv[t], xrowp + t * 256, m, acc);
+        }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();  // the next batch restages this wave's region
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    // 3. A column block's K parts in part order; element i of lane (r, g)
+    //    is pass row 4g + i.
+    if constexpr (KW > 1) {
+      *reinterpret_cast<f32x4*>(red + (wave * 64 + lane) * 4) = acc;
+      __syncthreads();
+    }
+    if (kw == 0 && n0 + r < n) {
+      f32x4 v = acc;
+#pragma unroll
+      for (int i = 1; i < KW; ++i) v = v + *reinterpret_cast<const f32x4*>(red + ((wave + i) * 64 + lane) * 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int mm = 4 * g + i;
+        if (mm < np) {
+          const int row = rlist[p0 + mm];
+          const uint32_t xrow = lhs ? lhs[row] : (uint32_t)row;
+          y[(size_t)row * n + n0 + r] = xrow < (uint32_t)x_rows ? TT::from_f32(v[i]) : (uint16_t)0;
+        }
+      }
+    }
+    if constexpr (KW > 1) __syncthreads();
+  }
+}
+
+template <typename TT, int BITS, int KW>
+hipError_t launch_dec(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
+                      const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
+                      unsigned int* status) {
+  const int S = k / 128;
+  const int steps_w = (S + KW - 1) / KW;
+  const int rows_max = std::min(kDecPass, n_rows);
+  const size_t lds = gather_decode_lds(n_rows, k, KW);
+  if (lds > 64 * 1024) {
+    static const hipError_t attr = [] {
+      const void* fn = reinterpret_cast<const void*>(&gather_decode_kernel<TT, BITS, KW>);
+      hipFuncAttributes fa;
+      hipError_t e = hipFuncGetAttributes(&fa, fn);
+      if (e != hipSuccess) return e;
+      return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)(160 * 1024 - fa.sharedSizeBytes));
+    }();
+    if (attr != hipSuccess) return attr;
+  }
+  int gs_shift = 0;
+  while ((1 << gs_shift) < q.gs) ++gs_shift;
+  const int cols = 16 * (kDecWaves / KW);
+  hipLaunchKernelGGL((gather_decode_kernel<TT, BITS, KW>), dim3((unsigned)((n + cols - 1) / cols), (unsigned)n_rows),
+                     dim3(64 * kDecWaves), lds, s, q.w, static_cast<const uint16_t*>(q.scales),
+                     static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x), x_rows, lhs, rhs,
+                     n_rows, static_cast<uint16_t*>(y), n_experts, n, k, gs_shift, (int)sorted, rows_max, steps_w,
+                     status);
+  return hipGetLastError();
+}
+
+template <typename TT, int BITS>
+hipError_t launch_dec_w(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
+                        const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
+                        unsigned int* status) {
+  const int kw = gather_decode_kw(n_rows, n, k);
+  if (kw == 4) return launch_dec<TT, BITS, 4>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+  if (kw == 2) return launch_dec<TT, BITS, 2>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+  return launch_dec<TT, BITS, 1>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+}
+
+}  // namespace
+
+// Waves of a workgroup splitting K (the other factor of 4 splits columns):
+// the most that keep the grid (column blocks x slots) within what the CUs
+// hold at once, about 4 workgroups each, since every workgroup pays the same
+// chain of dependent round trips (routing, weights and activations, sum);
+// with a longer K fewer column blocks per workgroup keep more loads in
+// flight per CU.
+int gather_decode_kw(int n_rows, int n, int k) {
+  const long blocks = (n + 15) / 16;
+  for (int kw = 4; kw > 1; kw /= 2) {
+    const long wgs = (long)n_rows * ((blocks + (4 / kw) - 1) / (4 / kw));
+    if (wgs <= 1024) return kw;
+  }
+  (void)k;
+  return 1;
+}
+
+size_t gather_decode_lds(int n_rows, int k, int kw) {
+  const int S = k / 128;
+  const int steps_w = (S + kw - 1) / kw;
+  const int rows_max = std::min(kDecPass, n_rows);
+  return (size_t)kDecWaves * rows_max * std::min(steps_w, kDecPF) * 256 + (size_t)kDecWaves * 256 * sizeof(float) +
+         kDecMaxRows * sizeof(int);
+}
+
+bool gather_decode_supported(const QuantArgs& q, int n_rows, int n, int k) {
+  if (q.bits != 4 && q.bits != 8) return false;
+  if (n_rows < 1 || n_rows > kDecMaxRows) return false;
+  if (q.gs != 32 && q.gs != 64 && q.gs != 128) return false;
+  if (k % 128 != 0 || k < 128) return false;
+  if ((uint64_t)n * (uint64_t)k * q.bits / 8 >= (1ull << 31) - (1ull << 20)) return false;
+  if ((uint64_t)n * (uint64_t)(k / q.gs) * 2 >= (1ull << 31)) return false;
+  return gather_decode_lds(n_rows, k, gather_decode_kw(n_rows, n, k)) <= (size_t)160 * 1024 - 1024;
+}
+
+hipError_t launch_gather_decode(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
+                                const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
+                                unsigned int* status) {
+  if (q.dtype == CPQ_DTYPE_BF16) {
+    if (q.bits == 4)
+      return launch_dec_w<BF16, 4>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+    if (q.bits == 8)
+      return launch_dec_w<BF16, 8>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+  }
+  if (q.dtype == CPQ_DTYPE_F16) {
+    if (q.bits == 4)
+      return launch_dec_w<F16, 4>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+    if (q.bits == 8)
+      return launch_dec_w<F16, 8>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace cpq

@@ -1,24 +1,31 @@
 // cpq_affine_qmm_t_noalloc: the prefill op for callers that cannot allocate
 // device memory (code under HIP graph capture, tight serving loops, hosts
-// that forbid allocation after start-up).  Same validation, kernel choice and
-// numerics as cpq_affine_qmm_t on a session with the default scratch
-// capacity, but on a caller's hipStream_t and with no session: the split-K
-// arrival counters and fp32 partial tiles live in `scratch`, a file-scope
-// device array of kNoAllocScratchBytes that every GPU the library runs on
-// holds until the process ends.
+// that forbid allocation after start-up).  Same validation and numerics as
+// cpq_affine_qmm_t, but on a caller's hipStream_t and with no session: the
+// split-K arrival counters and fp32 partial tiles live in `scratch`, a
+// file-scope device array of kNoAllocScratchBytes that every GPU the library
+// runs on holds until the process ends.
+//
+// Kernel choice: the kernel (chosen by M, as cpq_affine_qmm_t chooses it)
+// and K split a session with the default scratch capacity would run,
+// whenever its scratch fits the array (then the output is bit-identical to
+// cpq_affine_qmm_t's); otherwise the plan the same planner makes for the
+// array's capacity (a smaller K split, or none), which differs from the
+// session op only in summation order.
 //
 // Nothing here allocates: the array's per-device address comes from
 // hipGetSymbolAddress (once per device, with that device current), the CU
 // count from hipDeviceGetAttribute, and the kernels are launched exactly as
-// for a session.  A shape whose kernel choice needs more scratch than the
-// array holds is refused with CPQ_ERR_BUFFER_TOO_LARGE before any launch.
+// for a session.  The device is the one the caller's stream belongs to (the
+// current device for the null stream).  A set-up failure is not remembered:
+// the next call tries again.
 //
 // Sharing: every call on a GPU uses that GPU's one array.  The arrival
-// counters start at zero (module load, and explicitly at set-up) and every
-// launch that completes leaves the counters it used at zero again; the
-// partial tiles are written before they are read within a launch.  Calls
-// that overlap on one GPU (two streams, or two host threads) race on the
-// array and must be serialised by the caller.
+// counters are zero from module load and every launch that completes leaves
+// the counters it used at zero again; the partial tiles are written before
+// they are read within a launch.  Calls that overlap on one GPU (two streams,
+// or two host threads) race on the array and must be serialised by the
+// caller.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -37,34 +44,41 @@ constexpr int kMaxDevices = 64;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 struct DeviceSlot {
-  std::once_flag once;
-  hipError_t status = hipSuccess;
+  std::mutex mu;
+  bool ready = false;
   void* ptr = nullptr;  // device address of `scratch` on this device
   int cu_count = 0;
 };
 DeviceSlot g_slots[kMaxDevices];
 
-// Per-device set-up on the first call with that device current: the array's
-// address on this device, its counters cleared (a kernel, so a stream that is
-// being captured records no memset), the CU count.
+// The slot of the device `stream` belongs to, set up on first use: the
+// array's address on that device (queried with that device current) and its
+// CU count.  Nothing is launched: the array is zero from module load.
 hipError_t device_slot(hipStream_t stream, DeviceSlot** out) {
   int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   DeviceSlot& slot = g_slots[dev];
-  std::call_once(slot.once, [&] {
+  std::lock_guard<std::mutex> lock(slot.mu);
+  if (!slot.ready) {
+    int cur = 0;
+    e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
     void* p = nullptr;
-    hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (r == hipSuccess) r = hipDeviceGetAttribute(&slot.cu_count, hipDeviceAttributeMultiprocessorCount, dev);
-    // The array is zero from module load; the clear re-establishes that
-    // explicitly.  Under graph capture it is recorded as a kernel node that
-    // runs ahead of the op at every replay, which is equally correct.
-    if (r == hipSuccess) r = zero_words(stream, p, kWideCounterBytes / 4);
-    if (r == hipSuccess) slot.ptr = p;
-    slot.status = r;
-  });
-  if (slot.status != hipSuccess) return slot.status;
+    int cus = 0;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (cur != dev) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
+    if (e != hipSuccess) return e;  // not remembered: the next call tries again
+    slot.ptr = p;
+    slot.cu_count = cus;
+    slot.ready = true;
+  }
   *out = &slot;
   return hipSuccess;
 }
@@ -92,17 +106,12 @@ extern "C" cpq_status cpq_affine_qmm_t_noalloc(void* hip_stream, cpq_dtype dtype
   hipError_t e = cpq::device_slot(stream, &slot);
   if (e != hipSuccess) return cpq::hip_fail(e, "affine_qmm_t_noalloc: static scratch set-up");
   const cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
-  // The kernel a session with the default scratch capacity would run; the
-  // static array must hold what that kernel uses.
-  const cpq::QmmPlan plan =
-      cpq::qmm_plan(q, (int)m, (int)n, (int)k, slot->cu_count, cpq::kDefaultSessionScratchBytes);
-  if (plan.scratch_bytes > cpq::kNoAllocScratchBytes)
-    return fail(CPQ_ERR_BUFFER_TOO_LARGE,
-                "affine_qmm_t_noalloc: M=" + std::to_string(m) + ", N=" + std::to_string(n) + ", K=" +
-                    std::to_string(k) + " runs a K split of " + std::to_string(plan.split) + " whose partial tiles need " +
-                    std::to_string(plan.scratch_bytes) + " bytes of scratch; the static scratch holds " +
-                    std::to_string(cpq::kNoAllocScratchBytes) + " (use cpq_affine_qmm_t on a session)");
-  e = cpq::launch_qmm(stream, plan, slot->ptr, q, x, y, (int)m, (int)n, (int)k);
+  // The kernel a session with the default scratch capacity would run (chosen
+  // by M as affine_qmm_t chooses it) when its scratch fits the static array;
+  // else the plan made for the array's capacity.
+  const cpq::ExecCtx ex{stream, slot->cu_count, slot->ptr, cpq::kDefaultSessionScratchBytes,
+                        cpq::kNoAllocScratchBytes};
+  e = cpq::launch_matmul(ex, q, x, y, (int)m, (int)n, (int)k);
   if (e != hipSuccess) return cpq::hip_fail(e, "affine_qmm_t_noalloc launch");
   return CPQ_OK;
 }

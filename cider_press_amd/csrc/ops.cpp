@@ -33,10 +33,7 @@ bool kernel_available(cpq_dtype dtype, uint32_t group_size, uint32_t bits) {
 // row) never take them.
 int skinny_max_m(const QuantArgs& q, int n, int k) {
   if (!skinny_fits(k, (int)q.gs)) return 0;  // its slab constants would not fit in LDS
-  static const int lim = [] {
-    const char* e = std::getenv("CPQ_SKINNY_MAX_M");
-    return e && *e ? std::atoi(e) : 0;
-  }();
+  const int lim = env_int("CPQ_SKINNY_MAX_M", 0);  // tuning and test hook
   if (lim > 0) return lim;
   return n <= 8192 ? 64 : 32;
 }
@@ -101,6 +98,52 @@ bool mul_ok(size_t a, size_t b, size_t* out) {
 }  // namespace cpq
 
 using cpq::fail;
+
+namespace cpq {
+
+// Y[M, N] = X[M, K] . W^T on validated operands: the kernel the shape runs
+// best on.  Up to skinny_max_m rows: at K = 4096 / 8192 / 16384 (4/8-bit, up
+// to 16 rows) the decode kernel's layout with M activation rows; other
+// 4/8-bit shapes with K a multiple of 256 the tiled small-M kernel; other
+// shapes the slab kernel.  Larger M: the prefill plan.  Plans are made for
+// ex.plan_bytes of scratch and, when that plan needs more than the
+// ex.scratch_bytes at hand, for ex.scratch_bytes.  CPQ_SMALL_M=0 forces the
+// slab kernel, CPQ_QMV_ROWS=0 skips the decode layout (tuning hooks).
+hipError_t launch_matmul(const ExecCtx& ex, const QuantArgs& q, const void* x, void* y, int m, int n, int k) {
+  if (m <= skinny_max_m(q, n, k)) {
+    const bool small_on = env_int("CPQ_SMALL_M", 1) != 0;
+    const bool rows_on = env_int("CPQ_QMV_ROWS", 1) != 0;
+    const bool words4 = ((reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases)) & 3u) == 0;
+    SmallPlan sp{0, 0, 0, 0, 0};
+    if (small_on && aligned16(x) && aligned16(q.w) && words4) {
+      sp = qmm_small_plan(q, m, n, k, ex.cu_count, ex.plan_bytes);
+      if (sp.split > 0 && sp.scratch_bytes > ex.scratch_bytes)
+        sp = qmm_small_plan(q, m, n, k, ex.cu_count, ex.scratch_bytes);
+    }
+    if (small_on && rows_on && qmv_rows_fits(q, m, n, k, x)) return launch_qmv_rows(ex.stream, q, x, y, m, n, k);
+    if (sp.split > 0) return launch_qmm_small(ex.stream, sp, ex.scratch, q, x, y, m, n, k);
+    return launch_qmm_skinny(ex.stream, q, x, y, m, n, k);
+  }
+  QmmPlan plan = qmm_plan(q, m, n, k, ex.cu_count, ex.plan_bytes);
+  if (plan.scratch_bytes > ex.scratch_bytes) plan = qmm_plan(q, m, n, k, ex.cu_count, ex.scratch_bytes);
+  return launch_qmm(ex.stream, plan, ex.scratch, q, x, y, m, n, k);
+}
+
+ExecCtx session_ctx(const cpq_commands* cmds) {
+  const size_t cap = cmds->scratch ? cmds->scratch_bytes : 0;
+  return ExecCtx{cmds->stream, cmds->dev ? cmds->dev->cu_count : 0, cmds->scratch, cap, cap};
+}
+
+namespace {
+
+cpq_status route_matmul(cpq_commands* cmds, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
+                        const char* op) {
+  const std::string what = std::string(op) + (m <= skinny_max_m(q, n, k) ? " (small-M) launch" : " (prefill) launch");
+  return launched(launch_matmul(session_ctx(cmds), q, x, y, m, n, k), what.c_str());
+}
+
+}  // namespace
+}  // namespace cpq
 
 extern "C" {
 
@@ -392,45 +435,11 @@ cpq_status cpq_affine_qmm_t(cpq_commands* cmds, cpq_dtype dtype, const uint32_t*
   st = cpq::check_ptrs("affine_qmm_t", w_q, scales, biases, x, y);
   if (st != CPQ_OK) return st;
   cpq::QuantArgs q{w_q, scales, biases, (int)group_size, (int)bits, dtype};
-  return cpq::launched(cpq::launch_session_qmm(cmds, q, x, y, (int)m, (int)n, (int)k), "affine_qmm_t launch");
+  // The kernel is chosen by M as for the runtime node (small-M kernels, else
+  // the prefill plan): a caller of the op gets the same speed at a given
+  // shape whichever entry point it uses.
+  return cpq::route_matmul(cmds, q, x, y, (int)m, (int)n, (int)k, "affine_qmm_t");
 }
-
-namespace cpq {
-namespace {
-
-// Y[M, N] = X[M, K] . W^T for M > 1 on validated operands: the kernel the
-// shape runs best on.  Up to 16 rows at K = 4096 / 8192 / 16384 (4/8-bit):
-// the decode kernel's layout with M activation rows.  Other small-M 4/8-bit
-// shapes with K a multiple of 256: the tiled small-M kernel.  Other small-M
-// shapes: the slab kernel.  Larger M: the prefill plan.  CPQ_SMALL_M=0
-// forces the slab kernel, CPQ_QMV_ROWS=0 skips the decode layout (tuning
-// hooks, read once per process).
-cpq_status route_matmul(cpq_commands* cmds, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
-                        const char* op) {
-  const std::string what = std::string(op) + (m <= skinny_max_m(q, n, k) ? " (small-M) launch" : " (prefill) launch");
-  if (m <= skinny_max_m(q, n, k)) {
-    static const bool small_on = [] {
-      const char* e = std::getenv("CPQ_SMALL_M");
-      return !(e && *e == '0');
-    }();
-    const bool words4 = ((reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases)) & 3u) == 0;
-    const SmallPlan sp = small_on && aligned16(x) && aligned16(q.w) && words4
-                             ? qmm_small_plan(q, m, n, k, cmds->dev->cu_count, cmds->scratch ? cmds->scratch_bytes : 0)
-                             : SmallPlan{0, 0, 0, 0, 0};
-    static const bool rows_on = [] {
-      const char* e = std::getenv("CPQ_QMV_ROWS");
-      return !(e && *e == '0');
-    }();
-    if (small_on && rows_on && qmv_rows_fits(q, m, n, k, x))
-      return launched(launch_qmv_rows(cmds->stream, q, x, y, m, n, k), what.c_str());
-    if (sp.split > 0) return launched(launch_qmm_small(cmds->stream, sp, cmds->scratch, q, x, y, m, n, k), what.c_str());
-    return launched(launch_qmm_skinny(cmds->stream, q, x, y, m, n, k), what.c_str());
-  }
-  return launched(launch_session_qmm(cmds, q, x, y, m, n, k), what.c_str());
-}
-
-}  // namespace
-}  // namespace cpq
 
 // ---------------------------------------------------------------------------
 // Batched forms (MLX's `batched` kernels, adjust_matrix_offsets in
@@ -797,22 +806,39 @@ cpq_status cpq_affine_gather_qmm(cpq_commands* cmds, cpq_dtype dtype, const void
                        "affine_gather_qmm launch");
 }
 
-cpq_status cpq_stream_read(cpq_commands* cmds, const void* const* regions, const size_t* bytes, int n_regions,
-                           uint32_t* sink, int n_workgroups) {
+cpq_status cpq_stream_read_variant(cpq_commands* cmds, const void* const* regions, const size_t* bytes,
+                                   int n_regions, uint32_t* sink, int n_workgroups, int variant) {
   if (!cmds) return fail(CPQ_ERR_INVALID_ARGUMENT, "stream_read: NULL command session");
   if (n_regions < 1 || n_regions > 4 || !regions || !bytes)
     return fail(CPQ_ERR_INVALID_ARGUMENT, "stream_read: 1..=4 regions with their lengths");
   if (n_workgroups < 1 || n_workgroups > 65535)
     return fail(CPQ_ERR_INVALID_ARGUMENT, "stream_read: n_workgroups outside 1..=65535");
+  if (variant < 0 || variant >= cpq::stream_read_variant_count())
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "stream_read: variant outside 0..=" +
+                                              std::to_string(cpq::stream_read_variant_count() - 1));
   if (!sink || (reinterpret_cast<uintptr_t>(sink) & 3u))
     return fail(CPQ_ERR_INVALID_ARGUMENT, "stream_read: sink must be a 4-byte aligned device pointer");
-  for (int g = 0; g < n_regions; ++g)
+  uint64_t total = 0;
+  for (int g = 0; g < n_regions; ++g) {
     if ((bytes[g] && !regions[g]) || !cpq::aligned16(regions[g]) || bytes[g] % 16 != 0)
       return fail(CPQ_ERR_INVALID_ARGUMENT, "stream_read: region " + std::to_string(g) +
                                                 " must be 16-byte aligned with a length that is a multiple of 16");
-  return cpq::launched(cpq::launch_stream_read(cmds->stream, regions, bytes, n_regions, sink, n_workgroups),
+    total += bytes[g];
+  }
+  // The buffer-addressed designs cover one workgroup's span with a 32-bit
+  // byte range.
+  if (total / (uint64_t)n_workgroups + 16 >= (1ull << 32))
+    return fail(CPQ_ERR_INVALID_ARGUMENT, "stream_read: more than 4 GiB per workgroup");
+  return cpq::launched(cpq::launch_stream_read(cmds->stream, regions, bytes, n_regions, sink, n_workgroups, variant),
                        "stream_read launch");
 }
+
+cpq_status cpq_stream_read(cpq_commands* cmds, const void* const* regions, const size_t* bytes, int n_regions,
+                           uint32_t* sink, int n_workgroups) {
+  return cpq_stream_read_variant(cmds, regions, bytes, n_regions, sink, n_workgroups, 0);
+}
+
+int cpq_stream_read_variant_count(void) { return cpq::stream_read_variant_count(); }
 
 cpq_status cpq_quantized_matmul(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q,
                                 size_t w_q_len, const void* scales, size_t scales_len,

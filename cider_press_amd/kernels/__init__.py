@@ -237,7 +237,7 @@ class Commands:
     def end_capture(self) -> "Graph":
         g = ctypes.c_void_p()
         _lib.check(self._lib.cpq_commands_end_capture(self._h, ctypes.byref(g)))
-        return Graph(g)
+        return Graph(g, self)
 
     def __del__(self):
         if getattr(self, "_h", None) and self._lib is not None:
@@ -246,19 +246,31 @@ class Commands:
 
 
 class Graph:
-    """An instantiated HIP graph captured from a session."""
+    """An instantiated HIP graph captured from a session.
 
-    def __init__(self, handle):
+    The captured kernels address the capturing session's split-K scratch and
+    status word, so the graph keeps that session alive for as long as it
+    exists.  Release it (close) only when no replay is in flight."""
+
+    def __init__(self, handle, session: Commands):
         self._h = handle
         self._lib = _lib.lib()
+        self._session = session
 
     def launch(self, cmds: Commands) -> None:
+        if not self._h:
+            raise ValueError("graph_launch: the graph was released")
         _lib.check(self._lib.cpq_graph_launch(self._h, cmds.handle))
 
-    def __del__(self):
+    def close(self) -> None:
+        """Release the executable graph now (after its replays completed)."""
         if getattr(self, "_h", None) and self._lib is not None:
             self._lib.cpq_graph_release(self._h)
-            self._h = None
+        self._h = None
+        self._session = None
+
+    def __del__(self):
+        self.close()
 
 
 class Event:

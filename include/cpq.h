@@ -208,6 +208,15 @@ void cpq_event_release(cpq_event* ev);
 cpq_status cpq_stream_read(cpq_commands* cmds, const void* const* regions, const size_t* bytes, int n_regions,
                            uint32_t* sink, int n_workgroups);
 
+/* The same read in one of cpq_stream_read_variant_count() designs (variant 0
+ * is cpq_stream_read's): workgroups of 256, 512 or 1024 threads, 4, 8 or 16
+ * loads in flight per lane, plain or non-temporal loads, global or buffer
+ * addressing.  The benchmark takes the fastest as the ceiling.  At most
+ * 4 GiB per workgroup. */
+cpq_status cpq_stream_read_variant(cpq_commands* cmds, const void* const* regions, const size_t* bytes,
+                                   int n_regions, uint32_t* sink, int n_workgroups, int variant);
+int cpq_stream_read_variant_count(void);
+
 /* ------------------------------------------------------------------ */
 /* Quantization descriptor (runtime/src/quantization.rs:43-153)          */
 /* ------------------------------------------------------------------ */
@@ -241,7 +250,9 @@ cpq_status cpq_affine_qmv(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w
                           uint32_t group_size, uint32_t bits);
 
 /* affine_qmm_t_bf16 (qmm.rs:66-220), any T: Y[M,N] = X[M,K] . dequant(W[N,K])^T.
- * N % 32 == 0 is required as in the reference's aligned variant (qmm.rs:101-106). */
+ * N % 32 == 0 is required as in the reference's aligned variant (qmm.rs:101-106).
+ * The kernel is chosen by M as for cpq_quantized_matmul's M > 1 case
+ * (small-M kernels up to 64 rows, 32 past N = 8192; else the prefill plan). */
 cpq_status cpq_affine_qmm_t(cpq_commands* cmds, cpq_dtype dtype, const uint32_t* w_q,
                             size_t w_q_len, const void* scales, size_t scales_len,
                             const void* biases, size_t biases_len, const void* x, size_t x_len,
@@ -250,14 +261,18 @@ cpq_status cpq_affine_qmm_t(cpq_commands* cmds, cpq_dtype dtype, const uint32_t*
 
 /* affine_qmm_t for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, hosts that forbid allocation after
- * start-up).  No counterpart in the reference.  Same validation, kernel
- * choice and result as cpq_affine_qmm_t on a session with the default
- * scratch capacity, enqueued on the caller's hipStream_t without a session.
- * The split-K partial tiles and arrival counters live in a static device
- * array of 16 MiB + 64 KiB per GPU, held until the process ends; a shape
- * whose split needs more is refused with CPQ_ERR_BUFFER_TOO_LARGE before any
- * launch.  It calls no allocator.  Calls that overlap on one GPU (two streams
- * or threads) share that array and race: serialise them. */
+ * start-up).  No counterpart in the reference.  Same validation and numerics
+ * as cpq_affine_qmm_t, enqueued on the caller's hipStream_t without a
+ * session.  The split-K partial tiles and arrival counters live in a static
+ * device array of 16 MiB + 64 KiB per GPU, held until the process ends.  The
+ * kernel (chosen by M as for cpq_affine_qmm_t) is the one a default session
+ * runs whenever its K split fits that array (then the result is
+ * bit-identical); otherwise the best plan for the
+ * array's capacity (a smaller split or none: same tolerance, another
+ * summation order).  The stream must belong to a device of this process (the
+ * current device for the null stream); the array of that device is used.  It
+ * calls no allocator.  Calls that overlap on one GPU (two streams or
+ * threads) share that array and race: serialise them. */
 cpq_status cpq_affine_qmm_t_noalloc(void* hip_stream, cpq_dtype dtype, const uint32_t* w_q, size_t w_q_len,
                                     const void* scales, size_t scales_len, const void* biases, size_t biases_len,
                                     const void* x, size_t x_len, void* y, size_t y_len, size_t m, size_t n,

@@ -300,10 +300,10 @@ def test_small_m_long_k(device, library, oracle, m, n, k, gs):
 
 
 def test_gather_per_slab_long_k(device, library, oracle):
-    """The per-slab routed kernel (K beyond the expert-major kernel's LDS) with
-    98 KiB of slab constants."""
+    """The per-slab routed kernel (K beyond the expert-major kernel's LDS, and
+    more rows than the decode kernel takes) with 98 KiB of slab constants."""
     rng = np.random.default_rng(12288)
-    e, n, k, gs, rows = 2, 64, 12288, 32, 10
+    e, n, k, gs, rows = 2, 64, 12288, 32, 70
     w_q, s, b = _experts(rng, e, n, k, gs, 4, "bf16")
     x = make_x(rng, rows, k, "bf16")
     rhs = rng.integers(0, e, size=rows).astype(np.uint32)
@@ -324,6 +324,9 @@ def _use_kernel(monkeypatch, kern):
     dma, wide = _KERNEL_ENV[kern]
     monkeypatch.setenv("CPQ_QMM_DMA", dma)
     monkeypatch.setenv("CPQ_QMM_WIDE", wide)
+    # affine_qmm_t sends small M to the small-M kernels; these tests force
+    # the prefill kernels at every M.
+    monkeypatch.setenv("CPQ_SKINNY_MAX_M", "1")
 
 
 @pytest.mark.parametrize("kern", ["dma", "wide"])
@@ -525,9 +528,10 @@ def test_gather_expert_kernel_passes(device, library, oracle, bits, k, dtype):
 ])
 def test_gather_scale_bias_step_groupings(device, library, oracle, gs, k, dtype, bits, n):
     """Every scale / bias load grouping of the expert-major kernel, with
-    several slabs per wave (3 experts) and sorted routing."""
+    several slabs per wave (3 experts) and sorted routing (80 rows: past the
+    decode kernel's 64)."""
     rng = np.random.default_rng(gs + k + bits + n)
-    e, rows = 3, 60
+    e, rows = 3, 80
     w_q, s, b = _experts(rng, e, n, k, gs, bits, dtype)
     x = make_x(rng, 30, k, dtype)
     rhs = np.sort(rng.integers(0, e, size=rows)).astype(np.uint32)
