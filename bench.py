@@ -101,8 +101,13 @@ def copies_for(copy_bytes, target=ROTATE_BYTES):
     return int(max(2, -(-target // max(int(copy_bytes), 1))))
 
 
+REPS_OVERRIDE = 0
+
+
 def reps_for(steps):
-    """Timed replays: at least 10, more for short graphs."""
+    """Timed replays: at least 10, more for short graphs (or --reps)."""
+    if REPS_OVERRIDE > 0:
+        return REPS_OVERRIDE
     return int(max(10, min(100, 2000 // max(steps, 1))))
 
 
@@ -348,7 +353,8 @@ def bench_qmv(h, lib, args, rng, ceil):
     nbytes = algo_bytes(1, n, k, gs, bits)
     # Ceiling: every read design x grid over the same rotated bytes.
     c = ceil.measure(_wsb_regions(rot, X), args.steps, args.warmup,
-                     variants=range(h.L.cpq_stream_read_variant_count()))
+                     variants=range(h.L.cpq_stream_read_variant_count()) if not args.no_ceiling else (1,),
+                     grids=None if not args.no_ceiling else (1024,))
     ceil.best_variant = c["variant"]
     c["what"] = ("plain streaming read of the same rotated copies (W, scales, biases, x) in one launch per "
                  "step, best over read designs x grids")
@@ -464,12 +470,18 @@ def bench_configs(h, lib, args, rng, ceil):
 
     steps, warm = args.config_steps, args.warmup
     res = {}
+    pats = [p for p in (args.rows or "").split(",") if p]
+
+    def want(name):
+        return not pats or any(p in name for p in pats)
 
     def hbm(nb, us):
         gbs = nb / (us * 1e-6) / 1e9
         return round(gbs, 1), round(gbs / HBM_PEAK_GBS, 4)
 
     def with_ceiling(row, rot, x_buf, nb, regions=None):
+        if args.no_ceiling:
+            return row
         c = ceil.measure(regions or _wsb_regions(rot, x_buf), max(10, steps // 2), warm,
                          grids=(512, 1024, 2048, 4096))
         row["ceiling_us"] = c["us"]
@@ -532,23 +544,29 @@ def bench_configs(h, lib, args, rng, ceil):
                "copies": rot.n_copies, "working_set_MB": rot.working_set_mb, "parity": par}
         return row, rot, X, nb
 
-    res["cfg1"] = qmv_case("cfg1", 2048, 2048, "f16", bias_noise=1e-3)
-    res["cfg2b"] = qmv_case("cfg2b", 4096, 12288, "bf16")
+    if want("cfg1"):
+        res["cfg1"] = qmv_case("cfg1", 2048, 2048, "f16", bias_noise=1e-3)
+    if want("cfg2b"):
+        res["cfg2b"] = qmv_case("cfg2b", 4096, 12288, "bf16")
     for name, m, n, k, bits in (("cfg3b", 512, 12288, 4096, 4), ("cfg3c_n4096", 2048, 4096, 4096, 4),
                                 ("cfg3c_n12288", 2048, 12288, 4096, 4), ("qmm_8bit_m512", 512, 4096, 4096, 8)):
-        row, _, _, _ = qmm_case(name, m, n, k, bits=bits)
-        res[name] = row
+        if want(name):
+            row, _, _, _ = qmm_case(name, m, n, k, bits=bits)
+            res[name] = row
 
     # cfg4: small M through the routed op (eval.rs routing), K = N = 4096.
     rows = []
     n = k = 4096
     for bits, gs in ((4, 64), (4, 32), (8, 64)):
         for m in (1, 4, 16, 64):
+            if not want(f"cfg4_{bits}b_gs{gs}_m{m}"):
+                continue
             row, rot, X, nb = qmm_case(f"cfg4_{bits}b_gs{gs}_m{m}", m, n, k, bits=bits, gs=gs, routed=True)
             row = {"bits": bits, "gs": gs, "m": m, **row}
             rows.append(with_ceiling(row, rot, X, nb))
             del rot
-    res["cfg4"] = rows
+    if rows:
+        res["cfg4"] = rows
 
     # cfg5: 128 experts, W_up [768, 2048] and W_down [2048, 768], 4b gs64;
     # 256 tokens routed top-8 (uniform, without replacement) -> 2048 rows;
@@ -556,6 +574,9 @@ def bench_configs(h, lib, args, rng, ceil):
     e, topk = 128, 8
     for proj, (n, k) in (("up", (768, 2048)), ("down", (2048, 768))):
         gs, bits = 64, 4
+        if not want(f"cfg5_{proj}") and not want(f"cfg5_decode_{proj}") and not any(
+                want(f"cfg5_decode_t{t}_{proj}") for t in (1, 4)):
+            continue
         rot = Rotation(h.dev, rng, e * n, k, gs, bits, "bf16")
         per_w, per_s = n * k // 8, n * (k // gs)
         for tokens in (256, 4, 1):
@@ -568,6 +589,8 @@ def bench_configs(h, lib, args, rng, ceil):
             Y = h.dev.alloc_buffer(nrows * n, "bf16")
             labels = (("unsorted", False), ("sorted", True)) if tokens == 256 else (("sorted", True),)
             for label, sorted_rows in labels:
+                if not want(f"cfg5_{proj}_{label}" if tokens == 256 else f"cfg5_decode_t{tokens}_{proj}"):
+                    continue
                 rhs = (route[order] if sorted_rows else route).astype(np.uint32)
                 lh = lhs[order] if sorted_rows else lhs
                 if proj == "down":
@@ -606,16 +629,22 @@ def bench_configs(h, lib, args, rng, ceil):
     # published M4 Max figures beside ours, and M = 39 prefill.
     ref_rows = []
     for k, n, label, xl, pub in REF_QMV_SHAPES:
+        if not want("reference_qmv"):
+            break
         row = qmv_case(label, n, k, "bf16", x_len=xl)
         ref_rows.append({"label": label, **row, "reference_M4_Max_GB/s": pub,
                          "ratio_to_reference": round(row["GB/s"] / pub, 2)})
-    res["reference_qmv_qwen2.5_0.5b"] = ref_rows
+    if ref_rows:
+        res["reference_qmv_qwen2.5_0.5b"] = ref_rows
     ref_rows = []
     for k, n, label in REF_QMM_SHAPES:
+        if not want("reference_qmm"):
+            break
         row, rot, X, nb = qmm_case(label, REF_QMM_M, n, k)
         ref_rows.append(with_ceiling({"label": label, **row}, rot, X, nb))
         del rot
-    res["reference_qmm_m39_qwen2.5_0.5b"] = ref_rows
+    if ref_rows:
+        res["reference_qmm_m39_qwen2.5_0.5b"] = ref_rows
     return res
 
 
@@ -822,6 +851,9 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the configs table")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense bf16 GEMM anchor")
     ap.add_argument("--no-graph", action="store_true", help="encode timed calls directly (no graph capture)")
+    ap.add_argument("--reps", type=int, default=0, help="timed replays per timing (0: by step count)")
+    ap.add_argument("--no-ceiling", action="store_true", help="skip the read-ceiling legs (kernel traces)")
+    ap.add_argument("--rows", default="", help="configs rows to run: comma-separated name substrings")
     ap.add_argument("--config-steps", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
@@ -841,6 +873,8 @@ def main():
         pmc_summary(*args.pmc_summary)
         return
 
+    global REPS_OVERRIDE
+    REPS_OVERRIDE = args.reps
     if args.gpus != 1:
         print(json.dumps({"error": f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported "
                                    "(the quantized-matmul path is measured on a single MI355X)"}))
