@@ -236,9 +236,13 @@ hipError_t launch_gather_expert(hipStream_t s, const QuantArgs& q, const void* x
 // Routed experts at decode shapes (kernels/gather_decode.hip): up to 64
 // rows, 4/8-bit, K % 128 == 0; one workgroup per (distinct expert, 16
 // columns); validates the indices itself.
-int gather_decode_kw(int n_rows, int n, int k);
-size_t gather_decode_lds(int n_rows, int k, int kw);
-bool gather_decode_supported(const QuantArgs& q, int n_rows, int n, int k);
+int gather_decode_kw(int slots, int n, int k);
+size_t gather_decode_lds(int rows_max, int k, int kw);
+// The same kernel as a small-M matmul (rows in passes of 8, one workgroup
+// per (column group, pass)): 1 <= M <= 64, 4/8-bit, K % 128 == 0.
+bool dense_small_supported(const QuantArgs& q, int m, int n, int k);
+hipError_t launch_dense_small(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k);
+bool gather_decode_supported(const QuantArgs& q, int x_rows, int n_rows, int n, int k);
 hipError_t launch_gather_decode(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
                                 const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
                                 unsigned int* status);

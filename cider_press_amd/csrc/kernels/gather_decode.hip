@@ -34,6 +34,7 @@
 //     together with descents of a routing declared sorted; no index is used
 //     to address memory before it is checked.
 #include <algorithm>
+#include <type_traits>
 
 #include "../cpq_internal.hpp"
 #include "common.hpp"
@@ -46,6 +47,7 @@ using namespace dev;
 constexpr int kDecPF = 8;       // steps of loads in flight per wave
 constexpr int kDecMaxRows = 64; // rows of one call (one lane each)
 constexpr int kDecPass = 4;     // rows of a slot per pass (decode slots hold one or two)
+constexpr int kDensePass = 8;   // rows per pass (workgroup) of the dense small-M form
 constexpr int kDecWaves = 4;    // waves per workgroup: KW split K, 4 / KW column blocks
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
@@ -79,8 +81,11 @@ __device__ __forceinline__ f32x4 dec_step(const uint32_t* wq, uint32_t sv, uint3
   return acc;
 }
 
-template <typename TT, int BITS, int KW>
-__global__ __launch_bounds__(64 * kDecWaves) void gather_decode_kernel(
+// DENSE: the same kernel as a small-M matmul (one weight matrix, rows
+// 0..n_rows-1 of x and y; lhs, rhs and status unused): slot u is then the
+// u-th pass of rows_max rows.
+template <typename TT, int BITS, int KW, bool DENSE>
+__global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(BITS == 4 ? 4 : 3))) void gather_decode_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     const uint16_t* __restrict__ x, int x_rows, const uint32_t* __restrict__ lhs, const uint32_t* __restrict__ rhs,
     int n_rows, uint16_t* __restrict__ y, int n_experts, int n, int k, int gs_shift, int sorted, int rows_max,
@@ -93,43 +98,52 @@ __global__ __launch_bounds__(64 * kDecWaves) void gather_decode_kernel(
   const int n0 = nw0 + 16 * cbl;         // first column of this wave's block
   const int u = blockIdx.y;
 
-  // 1. Routing: lane i holds row i's expert and activation row.
-  const bool in = lane < n_rows;
-  const uint32_t e = in ? rhs[lane] : 0xffffffffu;
-  const uint32_t xr = in ? (lhs ? lhs[lane] : (uint32_t)lane) : 0u;
-  const bool ev = in && e < (uint32_t)n_experts;
-  const bool lv = in && xr < (uint32_t)x_rows;
-  const uint64_t valid = ballot(ev);
-  uint64_t later = 0;  // rows naming an expert an earlier row already named
-  for (int j = 0; j < n_rows; ++j) {
-    const uint32_t ej = __builtin_amdgcn_readlane(e, j);
-    const uint64_t same = ballot(ev && e == ej);
-    later |= same & (~0ull << j << 1);
-  }
-  const uint64_t first = valid & ~later;
-  const int nuniq = __builtin_popcountll(first);
-  if (blockIdx.x == 0 && u == 0) {
-    const uint32_t nxt = (in && lane + 1 < n_rows) ? rhs[lane + 1] : 0xffffffffu;
-    const int bad = __builtin_popcountll(ballot(in && (!ev || !lv))) +
-                    (sorted ? __builtin_popcountll(ballot(lane + 1 < n_rows && e > nxt)) : 0);
-    if (wave == 0 && lane == 0 && bad) atomicAdd(status, (unsigned)bad);
-  }
-  if (u >= nuniq) {
-    if (u == nuniq) {  // zero this column block of rows with an out-of-range expert
-      const uint64_t badrows = ballot(in && !ev);
-      for (int t = threadIdx.x; t < 64 * 16 * CB; t += 64 * kDecWaves) {
-        const int r = t / (16 * CB), c = nw0 + t % (16 * CB);
-        if (((badrows >> r) & 1) && c < n) y[(size_t)r * n + c] = 0;
-      }
+  uint32_t eu = 0, xr = 0;
+  uint64_t rows = 0, lvmask = ~0ull;
+  int nr = 0, rowbase = 0;
+  if constexpr (DENSE) {
+    rowbase = u * rows_max;
+    nr = min(rows_max, n_rows - rowbase);
+  } else {
+    // 1. Routing: lane i holds row i's expert and activation row.
+    const bool in = lane < n_rows;
+    const uint32_t e = in ? rhs[lane] : 0xffffffffu;
+    xr = in ? (lhs ? lhs[lane] : (uint32_t)lane) : 0u;
+    const bool ev = in && e < (uint32_t)n_experts;
+    const bool lv = in && xr < (uint32_t)x_rows;
+    const uint64_t valid = ballot(ev);
+    lvmask = ballot(lv);  // rows whose activation index is in range
+    uint64_t later = 0;   // rows naming an expert an earlier row already named
+    for (int j = 0; j < n_rows; ++j) {
+      const uint32_t ej = __builtin_amdgcn_readlane(e, j);
+      const uint64_t same = ballot(ev && e == ej);
+      later |= same & (~0ull << j << 1);
     }
-    return;
+    const uint64_t first = valid & ~later;
+    const int nuniq = __builtin_popcountll(first);
+    if (blockIdx.x == 0 && u == 0) {
+      const uint32_t nxt = (in && lane + 1 < n_rows) ? rhs[lane + 1] : 0xffffffffu;
+      const int bad = __builtin_popcountll(ballot(in && (!ev || !lv))) +
+                      (sorted ? __builtin_popcountll(ballot(lane + 1 < n_rows && e > nxt)) : 0);
+      if (wave == 0 && lane == 0 && bad) atomicAdd(status, (unsigned)bad);
+    }
+    if (u >= nuniq) {
+      if (u == nuniq) {  // zero this column block of rows with an out-of-range expert
+        const uint64_t badrows = ballot(in && !ev);
+        for (int t = threadIdx.x; t < 64 * 16 * CB; t += 64 * kDecWaves) {
+          const int r = t / (16 * CB), c = nw0 + t % (16 * CB);
+          if (((badrows >> r) & 1) && c < n) y[(size_t)r * n + c] = 0;
+        }
+      }
+      return;
+    }
+    uint64_t fm = first;
+    for (int i = 0; i < u; ++i) fm &= fm - 1;
+    const int lead = __builtin_ctzll(fm);
+    eu = __builtin_amdgcn_readlane(e, lead);
+    rows = ballot(ev && e == eu);
+    nr = __builtin_popcountll(rows);
   }
-  uint64_t fm = first;
-  for (int i = 0; i < u; ++i) fm &= fm - 1;
-  const int lead = __builtin_ctzll(fm);
-  const uint32_t eu = __builtin_amdgcn_readlane(e, lead);
-  const uint64_t rows = ballot(ev && e == eu);
-  const int nr = __builtin_popcountll(rows);
 
   // 2. This wave's K range and weight stream of expert eu.
   const int G = k >> gs_shift;
@@ -146,6 +160,8 @@ __global__ __launch_bounds__(64 * kDecWaves) void gather_decode_kernel(
       (void*)(scales + (size_t)eu * egroups), 0, (int)((uint32_t)n * (uint32_t)G * 2u), 0x00020000);
   const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(biases + (size_t)eu * egroups), 0, (int)((uint32_t)n * (uint32_t)G * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t xs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)x, 0, (int)((uint32_t)x_rows * (uint32_t)k * 2u), 0x00020000);
   // Columns past N read zeros through the range check (offsets past 2^31,
   // beyond every range; never stored).
   const bool col_ok = n0 + r < n;
@@ -159,42 +175,73 @@ __global__ __launch_bounds__(64 * kDecWaves) void gather_decode_kernel(
   int* rlist = reinterpret_cast<int*>(red + kDecWaves * 256);                           // [64]
 
   // The slot's rows in order: rank -> row.
-  if ((rows >> lane) & 1) rlist[__builtin_popcountll(rows & ((1ull << lane) - 1))] = lane;
+  if constexpr (DENSE) {
+    if (lane < nr) rlist[lane] = rowbase + lane;
+  } else {
+    if ((rows >> lane) & 1) rlist[__builtin_popcountll(rows & ((1ull << lane) - 1))] = lane;
+  }
   __syncthreads();
 
   for (int p0 = 0; p0 < nr; p0 += rows_max) {
     const int np = min(rows_max, nr - p0);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int b0 = 0; b0 < nst; b0 += kDecPF) {
-      const int nb = min(kDecPF, nst - b0);
-      // 2a. Loads of this batch: weights, then (scale, bias) of each step.
-      uint32_t wq[kDecPF][BITS];
-      uint32_t sv[kDecPF], bv[kDecPF];
-#pragma unroll
-      for (int t = 0; t < kDecPF; ++t)
-        if (t < nb) {
-          dec_load<BITS>(wr, voff0 + (uint32_t)(b0 + t) * (16u * BITS), wq[t]);
-          const uint32_t gi = coff0 + (((uint32_t)(4 * (js + b0 + t) + g) * 32u) >> gs_shift);
-          sv[t] = __builtin_amdgcn_raw_buffer_load_b16(sr, gi * 2u, 0, 0);
-          bv[t] = __builtin_amdgcn_raw_buffer_load_b16(br, gi * 2u, 0, 0);
-        }
-      // 2b. Stage the pass's activation slices of this batch: row m, step t,
-      //     16-byte piece p (natural order) at slot p ^ m of the row's step.
+    // Steps per batch: 8 for one row, 4 for up to 4 rows, else 2; the
+    // pass's activation pieces of a batch (16 per row and step) then fit the
+    // XP slots per lane of the batch form that runs it (see batch below).
+    const int bmax = np == 1 ? 8 : np <= 4 ? 4 : 2;
+    // One batch of nb <= PF steps.  2a. The pass's activation slices (row m,
+    // step t, 16-byte piece p in natural order, stored at slot p ^ m of the
+    // row's step) are requested first: their addresses are known from the
+    // routing loads already (a row's activation index comes from the routing
+    // lane holding it by a lane shuffle).  2b. Then (scale, bias) of each
+    // step, then the weights: the vote needs only the former, and step t's
+    // multiply waits for its own weights alone.  Every load is issued in one
+    // straight run, the PF slots past nb at an offset past every range (they
+    // read zeros): loads under a branch would make the compiler wait for each
+    // step's data before issuing the next.
+    auto batch = [&](int b0, int nb, auto pfc) {
+      constexpr int PF = decltype(pfc)::value;
+      // PF 8 runs one row (<= 128 pieces), PF 4 up to 4 rows and PF 2 up to
+      // 8 (<= 256), PF 1 up to 8 (<= 128).
+      constexpr int XP = (PF == 8 || PF == 1) ? 2 : 4;
       const int pieces = np * nb * 16;
-      for (int q = lane; q < pieces; q += 64) {
-        const int m = q / (nb * 16), rem = q - m * (nb * 16), t = rem >> 4, pc = rem & 15;
-        const int row = rlist[p0 + m];
-        const uint32_t xrow = lhs ? lhs[row] : (uint32_t)row;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (xrow < (uint32_t)x_rows)
-          v = *reinterpret_cast<const u32x4*>(x + (size_t)xrow * k + (size_t)(js + b0 + t) * 128 + pc * 8);
-        *reinterpret_cast<u32x4*>(xw + m * RB + t * 256 + ((pc ^ m) << 4)) = interleave_x<BITS>(v);
+      u32x4 xv[XP];
+      int xdst[XP];
+#pragma unroll
+      for (int i = 0; i < XP; ++i) {
+        xdst[i] = -1;
+        if (i == 0 || 64 * i < pieces) {  // uniform
+          const int q = lane + 64 * i;
+          const int qc = q < pieces ? q : 0;
+          const int m = qc / (nb * 16), rem = qc - m * (nb * 16), t = rem >> 4, pc = rem & 15;
+          const int row = rlist[p0 + m];
+          const uint32_t xrow = lhs ? (uint32_t)__shfl((int)xr, row, 64) : (uint32_t)row;
+          xdst[i] = q < pieces ? m * RB + t * 256 + ((pc ^ m) << 4) : -1;
+          const uint32_t off = q < pieces && xrow < (uint32_t)x_rows
+                                   ? (xrow * (uint32_t)k + (uint32_t)(js + b0 + t) * 128u + (uint32_t)pc * 8u) * 2u
+                                   : 0x80000000u;
+          xv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xs, off, 0, 0));
+        }
       }
+      uint32_t wq[PF][BITS];
+      uint32_t sv[PF], bv[PF];
+#pragma unroll
+      for (int t = 0; t < PF; ++t) {
+        const uint32_t gi = coff0 + (((uint32_t)(4 * (js + b0 + t) + g) * 32u) >> gs_shift);
+        const uint32_t so = t < nb ? gi * 2u : 0x80000000u;
+        sv[t] = __builtin_amdgcn_raw_buffer_load_b16(sr, so, 0, 0);
+        bv[t] = __builtin_amdgcn_raw_buffer_load_b16(br, so, 0, 0);
+      }
+#pragma unroll
+      for (int t = 0; t < PF; ++t)
+        dec_load<BITS>(wr, t < nb ? voff0 + (uint32_t)(b0 + t) * (16u * BITS) : 0x80000000u, wq[t]);
+#pragma unroll
+      for (int i = 0; i < XP; ++i)
+        if (xdst[i] >= 0) *reinterpret_cast<u32x4*>(xw + xdst[i]) = interleave_x<BITS>(xv[i]);
       // 2c. Vote (within the wave) on the single-FMA dequantization.
       bool ok = true;
 #pragma unroll
-      for (int t = 0; t < kDecPF; ++t)
-        if (t < nb) ok &= fast_ok_bits<TT>(sv[t], bv[t]);
+      for (int t = 0; t < PF; ++t) ok &= t >= nb || fast_ok_bits<TT>(sv[t], bv[t]);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -204,7 +251,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void gather_decode_kernel(
       const int m = min(r, np - 1);
       const unsigned char* xrowp = xw + m * RB;
 #pragma unroll
-      for (int t = 0; t < kDecPF; ++t)
+      for (int t = 0; t < PF; ++t)
         if (t < nb) {
           acc = fast ? dec_step<TT, BITS, true>(wq[t], sv[t], bv[t], xrowp + t * 256, m, acc)
                      : dec_step<TT, BITS, false>(wq[t], sv[t], bv[t], xrowp + t * 256, m, acc);
@@ -212,6 +259,13 @@ __global__ __launch_bounds__(64 * kDecWaves) void gather_decode_kernel(
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();  // the next batch restages this wave's region
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    for (int b0 = 0; b0 < nst; b0 += bmax) {
+      const int nb = min(bmax, nst - b0);
+      if (nb > 4) batch(b0, nb, std::integral_constant<int, 8>{});
+      else if (nb > 2) batch(b0, nb, std::integral_constant<int, 4>{});
+      else if (nb > 1) batch(b0, nb, std::integral_constant<int, 2>{});
+      else batch(b0, nb, std::integral_constant<int, 1>{});
     }
     // 3. A column block's K parts in part order; element i of lane (r, g)
     //    is pass row 4g + i.
@@ -228,8 +282,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void gather_decode_kernel(
         const int mm = 4 * g + i;
         if (mm < np) {
           const int row = rlist[p0 + mm];
-          const uint32_t xrow = lhs ? lhs[row] : (uint32_t)row;
-          y[(size_t)row * n + n0 + r] = xrow < (uint32_t)x_rows ? TT::from_f32(v[i]) : (uint16_t)0;
+          y[(size_t)row * n + n0 + r] = ((lvmask >> row) & 1) ? TT::from_f32(v[i]) : (uint16_t)0;
         }
       }
     }
@@ -237,17 +290,18 @@ __global__ __launch_bounds__(64 * kDecWaves) void gather_decode_kernel(
   }
 }
 
-template <typename TT, int BITS, int KW>
+template <typename TT, int BITS, int KW, bool DENSE>
 hipError_t launch_dec(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
                       const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
                       unsigned int* status) {
   const int S = k / 128;
   const int steps_w = (S + KW - 1) / KW;
-  const int rows_max = std::min(kDecPass, n_rows);
-  const size_t lds = gather_decode_lds(n_rows, k, KW);
+  const int rows_max = DENSE ? std::min(kDensePass, n_rows) : std::min(kDecPass, n_rows);
+  const int slots = DENSE ? (n_rows + rows_max - 1) / rows_max : n_rows;
+  const size_t lds = gather_decode_lds(rows_max, k, KW);
   if (lds > 64 * 1024) {
     static const hipError_t attr = [] {
-      const void* fn = reinterpret_cast<const void*>(&gather_decode_kernel<TT, BITS, KW>);
+      const void* fn = reinterpret_cast<const void*>(&gather_decode_kernel<TT, BITS, KW, DENSE>);
       hipFuncAttributes fa;
       hipError_t e = hipFuncGetAttributes(&fa, fn);
       if (e != hipSuccess) return e;
@@ -259,22 +313,44 @@ hipError_t launch_dec(hipStream_t s, const QuantArgs& q, const void* x, int x_ro
   int gs_shift = 0;
   while ((1 << gs_shift) < q.gs) ++gs_shift;
   const int cols = 16 * (kDecWaves / KW);
-  hipLaunchKernelGGL((gather_decode_kernel<TT, BITS, KW>), dim3((unsigned)((n + cols - 1) / cols), (unsigned)n_rows),
-                     dim3(64 * kDecWaves), lds, s, q.w, static_cast<const uint16_t*>(q.scales),
-                     static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x), x_rows, lhs, rhs,
-                     n_rows, static_cast<uint16_t*>(y), n_experts, n, k, gs_shift, (int)sorted, rows_max, steps_w,
-                     status);
+  hipLaunchKernelGGL((gather_decode_kernel<TT, BITS, KW, DENSE>),
+                     dim3((unsigned)((n + cols - 1) / cols), (unsigned)slots), dim3(64 * kDecWaves), lds, s, q.w,
+                     static_cast<const uint16_t*>(q.scales), static_cast<const uint16_t*>(q.biases),
+                     static_cast<const uint16_t*>(x), x_rows, lhs, rhs, n_rows, static_cast<uint16_t*>(y), n_experts,
+                     n, k, gs_shift, (int)sorted, rows_max, steps_w, status);
   return hipGetLastError();
 }
 
-template <typename TT, int BITS>
+template <typename TT, int BITS, bool DENSE>
 hipError_t launch_dec_w(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
                         const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
                         unsigned int* status) {
-  const int kw = gather_decode_kw(n_rows, n, k);
-  if (kw == 4) return launch_dec<TT, BITS, 4>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
-  if (kw == 2) return launch_dec<TT, BITS, 2>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
-  return launch_dec<TT, BITS, 1>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+  const int slots = DENSE ? (n_rows + kDensePass - 1) / kDensePass : n_rows;
+  const int kw = gather_decode_kw(slots, n, k);
+  if (kw == 4)
+    return launch_dec<TT, BITS, 4, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+  if (kw == 2)
+    return launch_dec<TT, BITS, 2, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+  return launch_dec<TT, BITS, 1, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+}
+
+template <bool DENSE>
+hipError_t launch_dec_any(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
+                          const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
+                          unsigned int* status) {
+  if (q.dtype == CPQ_DTYPE_BF16) {
+    if (q.bits == 4)
+      return launch_dec_w<BF16, 4, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+    if (q.bits == 8)
+      return launch_dec_w<BF16, 8, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+  }
+  if (q.dtype == CPQ_DTYPE_F16) {
+    if (q.bits == 4)
+      return launch_dec_w<F16, 4, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+    if (q.bits == 8)
+      return launch_dec_w<F16, 8, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -286,6 +362,8 @@ hipError_t launch_dec_w(hipStream_t s, const QuantArgs& q, const void* x, int x_
 // with a longer K fewer column blocks per workgroup keep more loads in
 // flight per CU.
 int gather_decode_kw(int n_rows, int n, int k) {
+  const int forced = env_int("CPQ_DEC_KW", 0);  // tuning hook: 1, 2 or 4
+  if (forced == 1 || forced == 2 || forced == 4) return forced;
   const long blocks = (n + 15) / 16;
   for (int kw = 4; kw > 1; kw /= 2) {
     const long wgs = (long)n_rows * ((blocks + (4 / kw) - 1) / (4 / kw));
@@ -295,40 +373,45 @@ int gather_decode_kw(int n_rows, int n, int k) {
   return 1;
 }
 
-size_t gather_decode_lds(int n_rows, int k, int kw) {
+size_t gather_decode_lds(int rows_max, int k, int kw) {
   const int S = k / 128;
   const int steps_w = (S + kw - 1) / kw;
-  const int rows_max = std::min(kDecPass, n_rows);
   return (size_t)kDecWaves * rows_max * std::min(steps_w, kDecPF) * 256 + (size_t)kDecWaves * 256 * sizeof(float) +
          kDecMaxRows * sizeof(int);
 }
 
-bool gather_decode_supported(const QuantArgs& q, int n_rows, int n, int k) {
+bool gather_decode_supported(const QuantArgs& q, int x_rows, int n_rows, int n, int k) {
   if (q.bits != 4 && q.bits != 8) return false;
   if (n_rows < 1 || n_rows > kDecMaxRows) return false;
+  if (x_rows < 1 || (uint64_t)x_rows * (uint64_t)k * 2u >= (1ull << 31)) return false;  // x through one range
   if (q.gs != 32 && q.gs != 64 && q.gs != 128) return false;
   if (k % 128 != 0 || k < 128) return false;
   if ((uint64_t)n * (uint64_t)k * q.bits / 8 >= (1ull << 31) - (1ull << 20)) return false;
   if ((uint64_t)n * (uint64_t)(k / q.gs) * 2 >= (1ull << 31)) return false;
-  return gather_decode_lds(n_rows, k, gather_decode_kw(n_rows, n, k)) <= (size_t)160 * 1024 - 1024;
+  return gather_decode_lds(std::min(kDecPass, n_rows), k, gather_decode_kw(n_rows, n, k)) <=
+         (size_t)160 * 1024 - 1024;
 }
 
 hipError_t launch_gather_decode(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
                                 const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
                                 unsigned int* status) {
-  if (q.dtype == CPQ_DTYPE_BF16) {
-    if (q.bits == 4)
-      return launch_dec_w<BF16, 4>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
-    if (q.bits == 8)
-      return launch_dec_w<BF16, 8>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
-  }
-  if (q.dtype == CPQ_DTYPE_F16) {
-    if (q.bits == 4)
-      return launch_dec_w<F16, 4>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
-    if (q.bits == 8)
-      return launch_dec_w<F16, 8>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
-  }
-  return hipErrorInvalidValue;
+  return launch_dec_any<false>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+}
+
+bool dense_small_supported(const QuantArgs& q, int m, int n, int k) {
+  if (q.bits != 4 && q.bits != 8) return false;
+  if (q.dtype != CPQ_DTYPE_BF16 && q.dtype != CPQ_DTYPE_F16) return false;
+  if (m < 1 || m > kDecMaxRows || (uint64_t)m * (uint64_t)k * 2u >= (1ull << 31)) return false;
+  if (q.gs != 32 && q.gs != 64 && q.gs != 128) return false;
+  if (k % 128 != 0 || k < 128) return false;
+  if ((uint64_t)n * (uint64_t)k * q.bits / 8 >= (1ull << 31) - (1ull << 20)) return false;
+  if ((uint64_t)n * (uint64_t)(k / q.gs) * 2 >= (1ull << 31)) return false;
+  const int slots = (m + kDensePass - 1) / kDensePass;
+  return gather_decode_lds(std::min(kDensePass, m), k, gather_decode_kw(slots, n, k)) <= (size_t)160 * 1024 - 1024;
+}
+
+hipError_t launch_dense_small(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k) {
+  return launch_dec_any<true>(s, q, x, m, nullptr, nullptr, m, y, 1, n, k, false, nullptr);
 }
 
 }  // namespace cpq

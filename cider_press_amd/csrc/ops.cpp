@@ -110,6 +110,11 @@ namespace cpq {
 // ex.scratch_bytes at hand, for ex.scratch_bytes.  CPQ_SMALL_M=0 forces the
 // slab kernel, CPQ_QMV_ROWS=0 skips the decode layout (tuning hooks).
 hipError_t launch_matmul(const ExecCtx& ex, const QuantArgs& q, const void* x, void* y, int m, int n, int k) {
+  // CPQ_SMALL_DENSE=1 forces the decode kernel's dense form where it
+  // applies, 0 keeps it off (tuning hooks).
+  const int dense_env = env_int("CPQ_SMALL_DENSE", -1);
+  const bool dense_ok = dense_env != 0 && aligned16(x) && aligned16(q.w) && dense_small_supported(q, m, n, k);
+  if (dense_ok && dense_env == 1) return launch_dense_small(ex.stream, q, x, y, m, n, k);
   if (m <= skinny_max_m(q, n, k)) {
     const bool small_on = env_int("CPQ_SMALL_M", 1) != 0;
     const bool rows_on = env_int("CPQ_QMV_ROWS", 1) != 0;
@@ -121,6 +126,14 @@ hipError_t launch_matmul(const ExecCtx& ex, const QuantArgs& q, const void* x, v
         sp = qmm_small_plan(q, m, n, k, ex.cu_count, ex.scratch_bytes);
     }
     if (small_on && rows_on && qmv_rows_fits(q, m, n, k, x)) return launch_qmv_rows(ex.stream, q, x, y, m, n, k);
+    // The tiled kernel where it has a workgroup for every fourth CU at
+    // least; below that (few column tiles and a K that does not split), or
+    // where its K granularity does not fit, the dense form of the decode
+    // kernel (K in 128-element steps split over the waves of a workgroup,
+    // 8 rows per workgroup).
+    const long cus = ex.cu_count > 0 ? ex.cu_count : 256;
+    const long small_wgs = sp.split > 0 ? (long)sp.split * ((n + 16 * sp.mb - 1) / (16 * sp.mb)) : 0;
+    if (dense_ok && small_wgs * 4 < cus) return launch_dense_small(ex.stream, q, x, y, m, n, k);
     if (sp.split > 0) return launch_qmm_small(ex.stream, sp, ex.scratch, q, x, y, m, n, k);
     return launch_qmm_skinny(ex.stream, q, x, y, m, n, k);
   }

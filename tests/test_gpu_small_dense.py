@@ -1,0 +1,85 @@
+"""Small-M matmul through the dense form of the routed-decode kernel
+(kernels/gather_decode.hip: rows in passes of 8, K in 128-element steps split
+over the waves of a workgroup), checked against the oracle through the C ABI.
+
+affine_qmm_t sends a shape there when the tiled small-M kernel does not take
+it (K not a multiple of 256) or would leave most CUs idle (few column tiles
+and a K that does not split): the reference's own M = 39 benchmark shapes
+(Qwen2.5-0.5B projections, K = 896 and the down projection's K = 4864) are
+such shapes.  CPQ_SMALL_DENSE=1 forces the form for every shape it takes, so
+the quantizations, group sizes, ragged N, one-step K and the pass boundaries
+(M = 8, 9, 64) are covered here too.
+"""
+import numpy as np
+import pytest
+
+from cider_press_amd.kernels import qmm as kqmm
+from cider_press_amd.synthetic import make_weight, make_x
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(device, library, w_q, s, b, x, m, n, k, gs, bits, dtype):
+    W, S, B = (device.upload(w_q.reshape(-1), "u32"), device.upload(s.reshape(-1), dtype),
+               device.upload(b.reshape(-1), dtype))
+    X = device.upload(x.reshape(-1), dtype)
+    Y = device.upload(np.full(m * n, 0x7FC0, np.uint16), dtype)  # NaN fill: every output is written
+    cmds = device.commands()
+    kqmm.affine_qmm_t(cmds, library, W, S, B, X, Y, m, n, k, gs, bits)
+    cmds.commit_and_wait()
+    return Y.to_numpy().reshape(m, n)
+
+
+def _check(oracle, y, x, w_q, s, b, m, n, k, gs, bits, dtype, label):
+    ref = oracle.qmm_ref(x, w_q, s, b, m, n, k, gs, bits, dtype, threads=8)
+    rep = oracle.tolerance_report(y, ref, x, k, dtype)
+    assert rep["ok"], (label, rep)
+
+
+@pytest.mark.parametrize("n,k", [(896, 896), (128, 896), (4864, 896), (896, 4864)])
+def test_reference_m39_shapes(device, library, oracle, n, k):
+    """The reference's M = 39 prefill shapes on the default routing."""
+    m, gs, bits, dtype = 39, 64, 4, "bf16"
+    rng = np.random.default_rng(n + k)
+    w_q, s, b = make_weight(rng, n, k, gs, bits, dtype)
+    x = make_x(rng, m, k, dtype)
+    y = _run(device, library, w_q, s, b, x, m, n, k, gs, bits, dtype)
+    _check(oracle, y, x, w_q, s, b, m, n, k, gs, bits, dtype, f"M=39 N={n} K={k}")
+
+
+@pytest.mark.parametrize("m,n,k,gs,bits,dtype", [
+    (1, 512, 4096, 64, 4, "bf16"),
+    (7, 224, 896, 64, 4, "bf16"),      # N not a multiple of 64: the last column group partly empty
+    (8, 256, 2048, 32, 4, "f16"),      # one full pass
+    (9, 256, 2048, 128, 8, "bf16"),    # a second pass of one row
+    (39, 160, 4864, 64, 4, "bf16"),    # K of 38 steps: uneven wave ranges
+    (64, 96, 1024, 64, 8, "f16"),      # the row limit, 8 passes
+    (16, 32, 128, 32, 4, "bf16"),      # one step: waves without a K range
+    (33, 4096, 4096, 64, 4, "bf16"),   # config 4's shape
+])
+def test_forced_dense_form(device, library, oracle, monkeypatch, m, n, k, gs, bits, dtype):
+    monkeypatch.setenv("CPQ_SMALL_DENSE", "1")
+    rng = np.random.default_rng(m * 100 + n + k + bits)
+    w_q, s, b = make_weight(rng, n, k, gs, bits, dtype)
+    x = make_x(rng, m, k, dtype)
+    y = _run(device, library, w_q, s, b, x, m, n, k, gs, bits, dtype)
+    _check(oracle, y, x, w_q, s, b, m, n, k, gs, bits, dtype, f"dense {m}x{n}x{k} {bits}b gs{gs} {dtype}")
+
+
+def test_forced_dense_deterministic_and_near_tiled(device, library, oracle, monkeypatch):
+    """Same inputs, dense form vs the tiled small-M kernel: both accumulate in
+    fp32 over the same dequantized weights (in different orders), so they
+    agree to a couple of output ULPs; and the dense form is deterministic
+    (two calls, same bits)."""
+    m, n, k, gs = 24, 512, 4096, 64
+    rng = np.random.default_rng(5)
+    w_q, s, b = make_weight(rng, n, k, gs, 4, "bf16")
+    x = make_x(rng, m, k, "bf16")
+    monkeypatch.setenv("CPQ_SMALL_DENSE", "1")
+    y1 = _run(device, library, w_q, s, b, x, m, n, k, gs, 4, "bf16")
+    y2 = _run(device, library, w_q, s, b, x, m, n, k, gs, 4, "bf16")
+    assert np.array_equal(y1, y2)
+    monkeypatch.setenv("CPQ_SMALL_DENSE", "0")
+    y3 = _run(device, library, w_q, s, b, x, m, n, k, gs, 4, "bf16")
+    a, c = oracle.bits_to_f32(y1, "bf16"), oracle.bits_to_f32(y3, "bf16")
+    assert np.max(np.abs(a - c)) <= 2 * 2.0 ** -7 * max(1.0, float(np.max(np.abs(c))))
