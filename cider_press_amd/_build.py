@@ -33,7 +33,7 @@ SOURCES = [
     "kernels/qmm_dma.hip", "kernels/qmm_small.hip",
     "kernels/qmm_n.hip",
     "kernels/gather.hip",
-    "kernels/gather_decode.hip",
+    "kernels/gather_decode.hip", "kernels/qmm_rows.hip",
     "kernels/moe.hip",
     "kernels/stream_read.hip",
 ]

@@ -242,6 +242,12 @@ size_t gather_decode_lds(int rows_max, int k, int kw);
 // per (column group, pass)): 1 <= M <= 64, 4/8-bit, K % 128 == 0.
 bool dense_small_supported(const QuantArgs& q, int m, int n, int k);
 hipError_t launch_dense_small(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k);
+// Small-M kernel with the activation rows resident in LDS
+// (kernels/qmm_rows.hip): 1 <= M <= 64, M * K * 2 <= 78 KiB, 4/8-bit,
+// K % 128 == 0; one workgroup per 128 columns.
+bool qmm_rows_supported(const QuantArgs& q, int m, int n, int k);
+int qmm_rows_workgroups(int n);
+hipError_t launch_qmm_rows(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k);
 bool gather_decode_supported(const QuantArgs& q, int x_rows, int n_rows, int n, int k);
 hipError_t launch_gather_decode(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
                                 const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,

@@ -115,6 +115,17 @@ hipError_t launch_matmul(const ExecCtx& ex, const QuantArgs& q, const void* x, v
   const int dense_env = env_int("CPQ_SMALL_DENSE", -1);
   const bool dense_ok = dense_env != 0 && aligned16(x) && aligned16(q.w) && dense_small_supported(q, m, n, k);
   if (dense_ok && dense_env == 1) return launch_dense_small(ex.stream, q, x, y, m, n, k);
+  // The LDS-resident small-M kernel (all rows of X in LDS, one workgroup
+  // per 128 columns, each wave's loads in one batch up to K = 1024) where
+  // it has a workgroup for every second CU at least: short K and large N,
+  // such as a vocabulary projection at prefill.
+  // CPQ_SMALL_ROWS=1 forces it where it applies, 0 keeps it off (tuning
+  // hooks).
+  const long cus = ex.cu_count > 0 ? ex.cu_count : 256;
+  const int rows_env = env_int("CPQ_SMALL_ROWS", -1);
+  const bool rows_ok = rows_env != 0 && aligned16(x) && aligned16(q.w) && qmm_rows_supported(q, m, n, k);
+  if (rows_ok && (rows_env == 1 || (m >= 2 && k <= 1024 && 2L * qmm_rows_workgroups(n) >= cus)))
+    return launch_qmm_rows(ex.stream, q, x, y, m, n, k);
   if (m <= skinny_max_m(q, n, k)) {
     const bool small_on = env_int("CPQ_SMALL_M", 1) != 0;
     const bool rows_on = env_int("CPQ_QMV_ROWS", 1) != 0;
@@ -131,7 +142,6 @@ hipError_t launch_matmul(const ExecCtx& ex, const QuantArgs& q, const void* x, v
     // where its K granularity does not fit, the dense form of the decode
     // kernel (K in 128-element steps split over the waves of a workgroup,
     // 8 rows per workgroup).
-    const long cus = ex.cu_count > 0 ? ex.cu_count : 256;
     const long small_wgs = sp.split > 0 ? (long)sp.split * ((n + 16 * sp.mb - 1) / (16 * sp.mb)) : 0;
     if (dense_ok && small_wgs * 4 < cus) return launch_dense_small(ex.stream, q, x, y, m, n, k);
     if (sp.split > 0) return launch_qmm_small(ex.stream, sp, ex.scratch, q, x, y, m, n, k);

@@ -1,6 +1,7 @@
 """Small-M matmul through the dense form of the routed-decode kernel
 (kernels/gather_decode.hip: rows in passes of 8, K in 128-element steps split
-over the waves of a workgroup), checked against the oracle through the C ABI.
+over the waves of a workgroup) and through the LDS-resident small-M kernel
+(kernels/qmm_rows.hip), checked against the oracle through the C ABI.
 
 affine_qmm_t sends a shape there when the tiled small-M kernel does not take
 it (K not a multiple of 256) or would leave most CUs idle (few column tiles
@@ -83,3 +84,64 @@ def test_forced_dense_deterministic_and_near_tiled(device, library, oracle, monk
     y3 = _run(device, library, w_q, s, b, x, m, n, k, gs, 4, "bf16")
     a, c = oracle.bits_to_f32(y1, "bf16"), oracle.bits_to_f32(y3, "bf16")
     assert np.max(np.abs(a - c)) <= 2 * 2.0 ** -7 * max(1.0, float(np.max(np.abs(c))))
+
+
+def test_reference_lm_head_m39(device, library, oracle):
+    """The reference's M = 39 lm_head shape (N = 151936, K = 896) on the
+    default routing (the LDS-resident kernel), rows of every row block
+    checked."""
+    m, n, k, gs = 39, 151936, 896, 64
+    rng = np.random.default_rng(151936)
+    w_q, s, b = make_weight(rng, n, k, gs, 4, "bf16")
+    x = make_x(rng, m, k, "bf16")
+    y = _run(device, library, w_q, s, b, x, m, n, k, gs, 4, "bf16")
+    rows = np.array([0, 1, 15, 16, 31, 32, 38])
+    ref = oracle.qmm_ref(x[rows], w_q, s, b, len(rows), n, k, gs, 4, "bf16", threads=8)
+    rep = oracle.tolerance_report(y[rows], ref, x[rows], k, "bf16")
+    assert rep["ok"], rep
+
+
+# The LDS-resident small-M kernel (kernels/qmm_rows.hip): all M rows of X in
+# LDS, one workgroup per 128 columns, every dequantized slice feeding each
+# 16-row block.  CPQ_SMALL_ROWS=1 forces it where it applies.
+@pytest.mark.parametrize("m,n,k,gs,bits,dtype", [
+    (39, 4096, 896, 64, 4, "bf16"),    # the lm_head shape's rows and K
+    (1, 256, 128, 64, 4, "bf16"),      # one row, one step
+    (16, 160, 896, 32, 4, "f16"),      # N not a multiple of 128: a partly empty workgroup
+    (17, 512, 1024, 128, 8, "bf16"),   # a second row block of one row
+    (64, 384, 512, 64, 4, "bf16"),     # the row limit, 64 KiB of activations
+    (8, 512, 4096, 64, 4, "bf16"),     # 32 steps: four batches
+    (33, 256, 1152, 64, 8, "f16"),     # 9 steps: a batch of 8 and a batch of 1
+    (48, 128, 768, 32, 4, "bf16"),     # three full row blocks
+])
+def test_forced_rows_kernel(device, library, oracle, monkeypatch, m, n, k, gs, bits, dtype):
+    monkeypatch.setenv("CPQ_SMALL_ROWS", "1")
+    rng = np.random.default_rng(m * 1000 + n + k + bits)
+    w_q, s, b = make_weight(rng, n, k, gs, bits, dtype)
+    x = make_x(rng, m, k, dtype)
+    y = _run(device, library, w_q, s, b, x, m, n, k, gs, bits, dtype)
+    _check(oracle, y, x, w_q, s, b, m, n, k, gs, bits, dtype, f"rows {m}x{n}x{k} {bits}b gs{gs} {dtype}")
+
+
+def test_rows_kernel_deterministic_and_graph_replay(device, library, monkeypatch):
+    """Eager calls and replays of a captured call give the same bits."""
+    monkeypatch.setenv("CPQ_SMALL_ROWS", "1")
+    m, n, k, gs = 39, 1024, 896, 64
+    rng = np.random.default_rng(12)
+    w_q, s, b = make_weight(rng, n, k, gs, 4, "bf16")
+    x = make_x(rng, m, k, "bf16")
+    first = _run(device, library, w_q, s, b, x, m, n, k, gs, 4, "bf16")
+    W, S, B = (device.upload(w_q.reshape(-1), "u32"), device.upload(s.reshape(-1), "bf16"),
+               device.upload(b.reshape(-1), "bf16"))
+    X = device.upload(x.reshape(-1), "bf16")
+    Y = device.alloc_buffer(m * n, "bf16")
+    cmds = device.commands()
+    cmds.begin_capture()
+    kqmm.affine_qmm_t(cmds, library, W, S, B, X, Y, m, n, k, gs, 4)
+    gr = cmds.end_capture()
+    for _ in range(3):
+        Y.write(np.zeros(m * n, np.uint16))
+        gr.launch(cmds)
+        cmds.commit_and_wait()
+        assert np.array_equal(Y.to_numpy().reshape(m, n), first)
+    gr.close()
