@@ -239,9 +239,14 @@ hipError_t launch_gather_expert(hipStream_t s, const QuantArgs& q, const void* x
 int gather_decode_kw(int slots, int n, int k);
 size_t gather_decode_lds(int rows_max, int k, int kw);
 // The same kernel as a small-M matmul (rows in passes of 8, one workgroup
-// per (column group, pass)): 1 <= M <= 64, 4/8-bit, K % 128 == 0.
+// per (column group, pass)): 1 <= M <= 64, 4/8-bit, K a multiple of the
+// group size (a partial last 128-step is masked).  pad_exact: K split over
+// 4 waves or 1 (never 2), so that zero K-padding to the next multiple of 512
+// (zero weights, scales, biases and activations past the logical K) keeps
+// every wave's steps and leaves every output bit unchanged.
 bool dense_small_supported(const QuantArgs& q, int m, int n, int k);
-hipError_t launch_dense_small(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k);
+hipError_t launch_dense_small(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
+                              bool pad_exact = false);
 // Small-M kernel with the activation rows resident in LDS
 // (kernels/qmm_rows.hip): 1 <= M <= 64, M * K * 2 <= 78 KiB, 4/8-bit,
 // K % 128 == 0; one workgroup per 128 columns.

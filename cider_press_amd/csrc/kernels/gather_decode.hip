@@ -147,8 +147,12 @@ __global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(
 
   // 2. This wave's K range and weight stream of expert eu.
   const int G = k >> gs_shift;
-  const int S = k >> 7;  // steps of 128
-  const int js = (kw * S) / KW, je = ((kw + 1) * S) / KW;
+  const int S = (k + 127) >> 7;  // steps of 128 (the last one partial when K % 128 != 0)
+  // Wave kw takes steps [kw SW, (kw + 1) SW) of S, SW = ceil(S / KW): with
+  // KW = 4 (or 1), a K zero-padded to the next multiple of 512 keeps every
+  // wave's steps and adds only zero steps.
+  const int SW = (S + KW - 1) / KW;
+  const int js = min(kw * SW, S), je = min(js + SW, S);
   const int nst = je - js;
   const int r = lane & 15, g = lane >> 4;
   const uint32_t rowbytes = (uint32_t)k * BITS / 8u;
@@ -217,31 +221,36 @@ __global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(
           const int row = rlist[p0 + m];
           const uint32_t xrow = lhs ? (uint32_t)__shfl((int)xr, row, 64) : (uint32_t)row;
           xdst[i] = q < pieces ? m * RB + t * 256 + ((pc ^ m) << 4) : -1;
-          const uint32_t off = q < pieces && xrow < (uint32_t)x_rows
-                                   ? (xrow * (uint32_t)k + (uint32_t)(js + b0 + t) * 128u + (uint32_t)pc * 8u) * 2u
-                                   : 0x80000000u;
+          const uint32_t kk = (uint32_t)(js + b0 + t) * 128u + (uint32_t)pc * 8u;  // first element of the piece
+          const uint32_t off =
+              q < pieces && xrow < (uint32_t)x_rows && kk < (uint32_t)k ? (xrow * (uint32_t)k + kk) * 2u : 0x80000000u;
           xv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xs, off, 0, 0));
         }
       }
       uint32_t wq[PF][BITS];
       uint32_t sv[PF], bv[PF];
+      bool live[PF];
 #pragma unroll
       for (int t = 0; t < PF; ++t) {
-        const uint32_t gi = coff0 + (((uint32_t)(4 * (js + b0 + t) + g) * 32u) >> gs_shift);
-        const uint32_t so = t < nb ? gi * 2u : 0x80000000u;
+        // Chunk (4 step + g) of 32 elements; chunks past K (a partial last
+        // step) read zeros like the slots past the batch.
+        const uint32_t ck = (uint32_t)(4 * (js + b0 + t) + g) * 32u;
+        live[t] = t < nb && ck < (uint32_t)k;
+        const uint32_t gi = coff0 + (ck >> gs_shift);
+        const uint32_t so = live[t] ? gi * 2u : 0x80000000u;
         sv[t] = __builtin_amdgcn_raw_buffer_load_b16(sr, so, 0, 0);
         bv[t] = __builtin_amdgcn_raw_buffer_load_b16(br, so, 0, 0);
       }
 #pragma unroll
       for (int t = 0; t < PF; ++t)
-        dec_load<BITS>(wr, t < nb ? voff0 + (uint32_t)(b0 + t) * (16u * BITS) : 0x80000000u, wq[t]);
+        dec_load<BITS>(wr, live[t] ? voff0 + (uint32_t)(b0 + t) * (16u * BITS) : 0x80000000u, wq[t]);
 #pragma unroll
       for (int i = 0; i < XP; ++i)
         if (xdst[i] >= 0) *reinterpret_cast<u32x4*>(xw + xdst[i]) = interleave_x<BITS>(xv[i]);
       // 2c. Vote (within the wave) on the single-FMA dequantization.
       bool ok = true;
 #pragma unroll
-      for (int t = 0; t < PF; ++t) ok &= t >= nb || fast_ok_bits<TT>(sv[t], bv[t]);
+      for (int t = 0; t < PF; ++t) ok &= !live[t] || fast_ok_bits<TT>(sv[t], bv[t]);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -294,7 +303,7 @@ template <typename TT, int BITS, int KW, bool DENSE>
 hipError_t launch_dec(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
                       const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
                       unsigned int* status) {
-  const int S = k / 128;
+  const int S = (k + 127) / 128;
   const int steps_w = (S + KW - 1) / KW;
   const int rows_max = DENSE ? std::min(kDensePass, n_rows) : std::min(kDecPass, n_rows);
   const int slots = DENSE ? (n_rows + rows_max - 1) / rows_max : n_rows;
@@ -324,9 +333,10 @@ hipError_t launch_dec(hipStream_t s, const QuantArgs& q, const void* x, int x_ro
 template <typename TT, int BITS, bool DENSE>
 hipError_t launch_dec_w(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
                         const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
-                        unsigned int* status) {
+                        unsigned int* status, bool pad_exact) {
   const int slots = DENSE ? (n_rows + kDensePass - 1) / kDensePass : n_rows;
-  const int kw = gather_decode_kw(slots, n, k);
+  int kw = gather_decode_kw(slots, n, k);
+  if (pad_exact && kw == 2) kw = 4;
   if (kw == 4)
     return launch_dec<TT, BITS, 4, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
   if (kw == 2)
@@ -337,18 +347,18 @@ hipError_t launch_dec_w(hipStream_t s, const QuantArgs& q, const void* x, int x_
 template <bool DENSE>
 hipError_t launch_dec_any(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
                           const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
-                          unsigned int* status) {
+                          unsigned int* status, bool pad_exact = false) {
+  auto go = [&](auto tt, auto bits) {
+    return launch_dec_w<decltype(tt), decltype(bits)::value, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts,
+                                                                    n, k, sorted, status, pad_exact);
+  };
   if (q.dtype == CPQ_DTYPE_BF16) {
-    if (q.bits == 4)
-      return launch_dec_w<BF16, 4, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
-    if (q.bits == 8)
-      return launch_dec_w<BF16, 8, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+    if (q.bits == 4) return go(BF16{}, std::integral_constant<int, 4>{});
+    if (q.bits == 8) return go(BF16{}, std::integral_constant<int, 8>{});
   }
   if (q.dtype == CPQ_DTYPE_F16) {
-    if (q.bits == 4)
-      return launch_dec_w<F16, 4, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
-    if (q.bits == 8)
-      return launch_dec_w<F16, 8, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+    if (q.bits == 4) return go(F16{}, std::integral_constant<int, 4>{});
+    if (q.bits == 8) return go(F16{}, std::integral_constant<int, 8>{});
   }
   return hipErrorInvalidValue;
 }
@@ -374,7 +384,7 @@ int gather_decode_kw(int n_rows, int n, int k) {
 }
 
 size_t gather_decode_lds(int rows_max, int k, int kw) {
-  const int S = k / 128;
+  const int S = (k + 127) / 128;
   const int steps_w = (S + kw - 1) / kw;
   return (size_t)kDecWaves * rows_max * std::min(steps_w, kDecPF) * 256 + (size_t)kDecWaves * 256 * sizeof(float) +
          kDecMaxRows * sizeof(int);
@@ -403,15 +413,16 @@ bool dense_small_supported(const QuantArgs& q, int m, int n, int k) {
   if (q.dtype != CPQ_DTYPE_BF16 && q.dtype != CPQ_DTYPE_F16) return false;
   if (m < 1 || m > kDecMaxRows || (uint64_t)m * (uint64_t)k * 2u >= (1ull << 31)) return false;
   if (q.gs != 32 && q.gs != 64 && q.gs != 128) return false;
-  if (k % 128 != 0 || k < 128) return false;
+  if (k < q.gs || k % q.gs != 0) return false;  // whole groups; a partial last step is masked
   if ((uint64_t)n * (uint64_t)k * q.bits / 8 >= (1ull << 31) - (1ull << 20)) return false;
   if ((uint64_t)n * (uint64_t)(k / q.gs) * 2 >= (1ull << 31)) return false;
   const int slots = (m + kDensePass - 1) / kDensePass;
   return gather_decode_lds(std::min(kDensePass, m), k, gather_decode_kw(slots, n, k)) <= (size_t)160 * 1024 - 1024;
 }
 
-hipError_t launch_dense_small(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k) {
-  return launch_dec_any<true>(s, q, x, m, nullptr, nullptr, m, y, 1, n, k, false, nullptr);
+hipError_t launch_dense_small(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
+                              bool pad_exact) {
+  return launch_dec_any<true>(s, q, x, m, nullptr, nullptr, m, y, 1, n, k, false, nullptr, pad_exact);
 }
 
 }  // namespace cpq

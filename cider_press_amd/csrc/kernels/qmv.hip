@@ -842,6 +842,17 @@ hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, i
       }
     }
   }
+  if constexpr (BITS == 4 || BITS == 8) {
+    // Rows of up to 1024 elements (the lean kernel takes none of them; the
+    // reference's K = 896 projections and their K-padded twins): the
+    // routed-decode kernel's dense form with one row, K split so that a
+    // zero-padded K (896 -> 960 -> 1024) gives the same bits (lm_head,
+    // N = 151936: 32.8 -> 20 us).  CPQ_QMV_DENSE=0 keeps it off (tuning
+    // hook).
+    const bool al16 = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(q.w)) & 15u) == 0;
+    if (k <= 1024 && al16 && env_int("CPQ_QMV_DENSE", 1) != 0 && dense_small_supported(q, 1, n, k))
+      return launch_dense_small(s, q, x, y, 1, n, k, true);
+  }
   if (lds > 160 * 1024) {
     // Very long rows: the small-M kernel while its slab constants fit in LDS
     // (about 500 groups per row), beyond that a prefill kernel, which keeps

@@ -9,12 +9,14 @@ and a K that does not split): the reference's own M = 39 benchmark shapes
 (Qwen2.5-0.5B projections, K = 896 and the down projection's K = 4864) are
 such shapes.  CPQ_SMALL_DENSE=1 forces the form for every shape it takes, so
 the quantizations, group sizes, ragged N, one-step K and the pass boundaries
-(M = 8, 9, 64) are covered here too.
+(M = 8, 9, 64) are covered here too.  affine_qmv sends rows of up to 1024
+elements that its lean kernel does not take to the same form (M = 1).
 """
 import numpy as np
 import pytest
 
 from cider_press_amd.kernels import qmm as kqmm
+from cider_press_amd.kernels import qmv as kqmv
 from cider_press_amd.synthetic import make_weight, make_x
 
 pytestmark = pytest.mark.gpu
@@ -57,6 +59,9 @@ def test_reference_m39_shapes(device, library, oracle, n, k):
     (64, 96, 1024, 64, 8, "f16"),      # the row limit, 8 passes
     (16, 32, 128, 32, 4, "bf16"),      # one step: waves without a K range
     (33, 4096, 4096, 64, 4, "bf16"),   # config 4's shape
+    (5, 256, 960, 64, 4, "bf16"),      # K % 128 = 64: a half last step
+    (3, 128, 96, 32, 8, "f16"),        # K below one step
+    (12, 160, 992, 32, 4, "bf16"),     # K % 128 = 96
 ])
 def test_forced_dense_form(device, library, oracle, monkeypatch, m, n, k, gs, bits, dtype):
     monkeypatch.setenv("CPQ_SMALL_DENSE", "1")
@@ -145,3 +150,59 @@ def test_rows_kernel_deterministic_and_graph_replay(device, library, monkeypatch
         cmds.commit_and_wait()
         assert np.array_equal(Y.to_numpy().reshape(m, n), first)
     gr.close()
+
+
+@pytest.mark.parametrize("n,k,gs,bits,dtype", [
+    (4864, 896, 64, 4, "bf16"),     # the reference's gate/up decode shape
+    (151936, 896, 64, 4, "bf16"),   # its lm_head
+    (1000, 1024, 128, 8, "f16"),    # 8-bit, N not a multiple of 16
+    (96, 512, 32, 4, "bf16"),
+    (256, 992, 32, 4, "bf16"),      # K % 128 = 96
+])
+def test_qmv_short_k_dense_route(device, library, oracle, monkeypatch, n, k, gs, bits, dtype):
+    """affine_qmv on the dense form (default) and on its own kernels
+    (CPQ_QMV_DENSE=0): both within the tolerance of the oracle."""
+    rng = np.random.default_rng(n + k + bits)
+    w_q, s, b = make_weight(rng, n, k, gs, bits, dtype)
+    x = make_x(rng, 1, k, dtype)
+    W, S, B = (device.upload(w_q.reshape(-1), "u32"), device.upload(s.reshape(-1), dtype),
+               device.upload(b.reshape(-1), dtype))
+    X = device.upload(x.reshape(-1), dtype)
+    ref = oracle.qmm_ref(x, w_q, s, b, 1, n, k, gs, bits, dtype, threads=8)
+    for env in ("1", "0"):
+        monkeypatch.setenv("CPQ_QMV_DENSE", env)
+        Y = device.upload(np.full(n, 0x7FC0, np.uint16), dtype)
+        cmds = device.commands()
+        kqmv.affine_qmv(cmds, library, W, S, B, X, Y, k, gs, bits)
+        cmds.commit_and_wait()
+        rep = oracle.tolerance_report(Y.to_numpy().reshape(1, n), ref, x, k, dtype)
+        assert rep["ok"], (env, rep)
+
+
+@pytest.mark.parametrize("k_log,k_pads,gs", [(992, (1024,), 32), (640, (704, 768, 1024), 64)])
+def test_qmv_short_k_padding_bit_exact(device, library, k_log, k_pads, gs):
+    """K-padding contract on the short-K qmv route at more shapes: zero
+    weights, scales and biases past the logical K and a zero activation tail
+    give the unpadded output's bits."""
+    rng = np.random.default_rng(k_log)
+    n = 384
+    w_q, s, b = make_weight(rng, n, k_log, gs, 4, "bf16")
+    x = make_x(rng, 1, k_log, "bf16")
+
+    def run(wq, ss, bb, k):
+        W, S, B = (device.upload(wq.reshape(-1), "u32"), device.upload(ss.reshape(-1), "bf16"),
+                   device.upload(bb.reshape(-1), "bf16"))
+        xp = np.zeros(k, np.uint16); xp[:k_log] = x.reshape(-1)  # zero activation tail
+        X = device.upload(xp, "bf16")
+        Y = device.alloc_buffer(n, "bf16")
+        cmds = device.commands()
+        kqmv.affine_qmv(cmds, library, W, S, B, X, Y, k, gs, 4)
+        cmds.commit_and_wait()
+        return Y.to_numpy()
+
+    base = run(w_q, s, b, k_log)
+    for k in k_pads:
+        wp = np.zeros((n, k * 4 // 32), np.uint32); wp[:, :w_q.shape[1]] = w_q
+        sp = np.zeros((n, k // gs), np.uint16); sp[:, :s.shape[1]] = s
+        bp = np.zeros((n, k // gs), np.uint16); bp[:, :b.shape[1]] = b
+        assert np.array_equal(run(wp, sp, bp, k), base), k
