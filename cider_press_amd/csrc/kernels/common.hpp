@@ -246,6 +246,13 @@ __device__ __forceinline__ bool fast_quick_ok(const FastQuick& a) {
   else return fast_quick_ok_f16(a);
 }
 
+// Row key of the 16-slot XOR swizzle of activation rows in LDS: r (0..15)
+// with its two 2-bit halves swapped.  A 16-byte MFMA operand read serves
+// lanes p, p + 4, ..., p + 60 together (rows p, p + 4, p + 8, p + 12 of a
+// 16-row block, 4 lane groups); with key(r) = r those 16 lanes meet in 4
+// slots (4 bank-conflict cycles per read), with the swapped key in 16.
+__device__ __forceinline__ int swz_key(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
 // Natural 16-byte activation slice -> interleaved slot order of BITS.
 template <int BITS>
 __device__ __forceinline__ u32x4 interleave_x(u32x4 v) {

@@ -70,10 +70,11 @@ __device__ __forceinline__ f32x4 dec_step(const uint32_t* wq, uint32_t sv, uint3
   const float s = TT::to_f32((uint16_t)sv), b = TT::to_f32((uint16_t)bv);
   const float s16 = s * 0.0625f, c0 = fmaf(-1024.f, s, b), c1 = fmaf(-64.f, s, b);
   const int g4 = (threadIdx.x >> 4) & 3;
-  const u32x4 a0 = *reinterpret_cast<const u32x4*>(xrow + (((4 * g4 + 0) ^ m) << 4));
-  const u32x4 a1 = *reinterpret_cast<const u32x4*>(xrow + (((4 * g4 + 1) ^ m) << 4));
-  const u32x4 a2 = *reinterpret_cast<const u32x4*>(xrow + (((4 * g4 + 2) ^ m) << 4));
-  const u32x4 a3 = *reinterpret_cast<const u32x4*>(xrow + (((4 * g4 + 3) ^ m) << 4));
+  const int km = swz_key(m);
+  const u32x4 a0 = *reinterpret_cast<const u32x4*>(xrow + (((4 * g4 + 0) ^ km) << 4));
+  const u32x4 a1 = *reinterpret_cast<const u32x4*>(xrow + (((4 * g4 + 1) ^ km) << 4));
+  const u32x4 a2 = *reinterpret_cast<const u32x4*>(xrow + (((4 * g4 + 2) ^ km) << 4));
+  const u32x4 a3 = *reinterpret_cast<const u32x4*>(xrow + (((4 * g4 + 3) ^ km) << 4));
   acc = Mfma16<TT>::run(a0, dequant_slice<TT, BITS, FAST, 0>(wq, s, s16, b, c0, c1), acc);
   acc = Mfma16<TT>::run(a1, dequant_slice<TT, BITS, FAST, 1>(wq, s, s16, b, c0, c1), acc);
   acc = Mfma16<TT>::run(a2, dequant_slice<TT, BITS, FAST, 2>(wq, s, s16, b, c0, c1), acc);
@@ -194,7 +195,7 @@ __global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(
     // XP slots per lane of the batch form that runs it (see batch below).
     const int bmax = np == 1 ? 8 : np <= 4 ? 4 : 2;
     // One batch of nb <= PF steps.  2a. The pass's activation slices (row m,
-    // step t, 16-byte piece p in natural order, stored at slot p ^ m of the
+    // step t, 16-byte piece p in natural order, stored at slot p ^ swz_key(m) of the
     // row's step) are requested first: their addresses are known from the
     // routing loads already (a row's activation index comes from the routing
     // lane holding it by a lane shuffle).  2b. Then (scale, bias) of each
@@ -220,7 +221,7 @@ __global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(
           const int m = qc / (nb * 16), rem = qc - m * (nb * 16), t = rem >> 4, pc = rem & 15;
           const int row = rlist[p0 + m];
           const uint32_t xrow = lhs ? (uint32_t)__shfl((int)xr, row, 64) : (uint32_t)row;
-          xdst[i] = q < pieces ? m * RB + t * 256 + ((pc ^ m) << 4) : -1;
+          xdst[i] = q < pieces ? m * RB + t * 256 + ((pc ^ swz_key(m)) << 4) : -1;
           const uint32_t kk = (uint32_t)(js + b0 + t) * 128u + (uint32_t)pc * 8u;  // first element of the piece
           const uint32_t off =
               q < pieces && xrow < (uint32_t)x_rows && kk < (uint32_t)k ? (xrow * (uint32_t)k + kk) * 2u : 0x80000000u;

@@ -15,20 +15,20 @@
 //     16 (8 blockIdx.x + w) and walks all of K in 128-element steps;
 //   - the activation rows are copied into LDS once per workgroup by the
 //     buffer-to-LDS path (no VGPRs, natural element order): slot j of step t
-//     of row r holds 16-byte piece j ^ (r & 15) of that step, so the 16 rows
-//     of a row block read 16 distinct bank groups;
+//     of row r holds 16-byte piece j ^ swz_key(r & 15) of that step, so the
+//     16 lanes an operand read serves together hit 16 distinct slots;
 //   - lane (column r, chunk group g) loads, per step, the 32-element chunk g
 //     of its column (16 bytes at 4 bits) and its (scale, bias), and
 //     dequantizes it slice by slice in natural order into the B operand of
 //     v_mfma_f32_16x16x32 (B[k][n] in lane n + 16 (k / 8)); the A operand of
 //     row block rb is rows 16 rb .. 16 rb + 15 (rows past M read row M-1,
 //     never stored), D[m][n] in lane n + 16 (m / 4), element m % 4;
-//   - batches of up to 8 steps: each batch's (scale, bias) loads, then its
-//     weight loads, issued in one straight run (the batch body exists for 8,
-//     4, 2 and 1 steps; slots past the batch read at an offset past every
-//     range, which returns zeros), so a step's multiply waits for its own
-//     weights only; a vote within the wave picks the single-FMA
-//     dequantization for the batch.
+//   - batches of up to 8 steps (4 at 8 bits): each batch's (scale, bias)
+//     loads, then its weight loads, issued in one straight run (the batch
+//     body exists for 8, 4, 2 and 1 steps; slots past the batch read at an
+//     offset past every range, which returns zeros), so a step's multiply
+//     waits for its own weights only; a vote within the wave picks the
+//     single-FMA dequantization for the batch.
 #include <algorithm>
 #include <type_traits>
 
@@ -90,7 +90,7 @@ __device__ __forceinline__ void rows_step(const uint32_t (*wq)[BITS], const uint
     for (int rb = 0; rb < RBK; ++rb) {
       const int row = rows[rb];
       const u32x4 a =
-          *reinterpret_cast<const u32x4*>(xs + row * rstride + ((((4 * g + i) ^ (row & 15))) << 4));
+          *reinterpret_cast<const u32x4*>(xs + row * rstride + (((4 * g + i) ^ swz_key(row & 15)) << 4));
 #pragma unroll
       for (int c = 0; c < kRowsNCB; ++c) acc[rb][c] = Mfma16<TT>::run(a, bo[c], acc[rb][c]);
     }
@@ -123,13 +123,13 @@ __global__ __launch_bounds__(64 * kRowsWaves) __attribute__((amdgpu_waves_per_eu
 
   // 1. Activation rows into LDS, row r at byte r * rstride: copy i (64 lanes
   //    x 16 bytes, at byte 1024 i) is row i / SPR, steps 4 (i % SPR) + g;
-  //    lane (j, g) fills slot j of its step with piece j ^ (row & 15).  Steps
+  //    lane (j, g) fills slot j of its step with piece j ^ swz_key(row & 15).  Steps
   //    past K read zeros (offset past the range) into the row's rounding.
   const int ncopies = m * SPR;
   for (int i = wave; i < ncopies; i += kRowsWaves) {
     const int row = i / SPR;
     const int t = 4 * (i - row * SPR) + g;
-    const int pc = r ^ (row & 15);
+    const int pc = r ^ swz_key(row & 15);
     const uint32_t off =
         t < S ? ((uint32_t)row * (uint32_t)k + (uint32_t)t * 128u + (uint32_t)pc * 8u) * 2u : 0x80000000u;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(smem + 1024 * i), 16,
@@ -178,12 +178,29 @@ __global__ __launch_bounds__(64 * kRowsWaves) __attribute__((amdgpu_waves_per_eu
       wait_vmcnt<PF * kRowsNCB * (2 + BITS / 4)>();
       __syncthreads();
     }
-    bool ok = true;
+    // Vote: the packed exponent check over the batch's (scale, bias) pairs
+    // (two per word; slots past the batch repeat the first pair), and the
+    // exact per-group check only when some lane fails it.
+    FastQuick fq;
+    fast_quick_init(fq);
 #pragma unroll
-    for (int t = 0; t < PF; ++t)
+    for (int c = 0; c < kRowsNCB; ++c)
 #pragma unroll
-      for (int c = 0; c < kRowsNCB; ++c) ok &= t >= nb || fast_ok_bits<TT>(sv[t][c], bv[t][c]);
-    const bool fast = rows_ballot(!ok) == 0;
+      for (int t = 0; t < PF; t += 2) {
+        const int t1 = t + 1 < PF ? t + 1 : t;
+        const uint32_t s0 = t < nb ? sv[t][c] : sv[0][c], b0v = t < nb ? bv[t][c] : bv[0][c];
+        const uint32_t s1 = t1 < nb ? sv[t1][c] : sv[0][c], b1v = t1 < nb ? bv[t1][c] : bv[0][c];
+        fast_quick_add<TT>(fq, s0 | (s1 << 16), b0v | (b1v << 16));
+      }
+    bool fast = rows_ballot(!fast_quick_ok<TT>(fq)) == 0;
+    if (!fast) {
+      bool ok = true;
+#pragma unroll
+      for (int t = 0; t < PF; ++t)
+#pragma unroll
+        for (int c = 0; c < kRowsNCB; ++c) ok &= t >= nb || fast_ok_bits<TT>(sv[t][c], bv[t][c]);
+      fast = rows_ballot(!ok) == 0;
+    }
 #pragma unroll
     for (int t = 0; t < PF; ++t)
       if (t < nb) {

@@ -206,3 +206,29 @@ def test_qmv_short_k_padding_bit_exact(device, library, k_log, k_pads, gs):
         sp = np.zeros((n, k // gs), np.uint16); sp[:, :s.shape[1]] = s
         bp = np.zeros((n, k // gs), np.uint16); bp[:, :b.shape[1]] = b
         assert np.array_equal(run(wp, sp, bp, k), base), k
+
+
+# Scale / bias pairs outside the single-FMA dequantization's exactness range
+# (a tiny scale under a much larger bias; an f16 subnormal scale), zero
+# scales or biases (they fail the packed exponent check and pass the exact
+# one) and a -0 bias under a negative scale (fails both).
+_SLOW_SB = {"bf16": (0x3000, 0x3C23), "f16": (0x0001, 0x211F)}
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("form", ["rows", "dense"])
+def test_small_forms_slow_and_zero_groups(device, library, oracle, monkeypatch, dtype, form):
+    monkeypatch.setenv("CPQ_SMALL_ROWS" if form == "rows" else "CPQ_SMALL_DENSE", "1")
+    m, n, k, gs = 20, 256, 896, 64
+    rng = np.random.default_rng(21)
+    w_q, s, b = make_weight(rng, n, k, gs, 4, dtype)
+    s[17, 2], b[17, 2] = _SLOW_SB[dtype]
+    s[200, k // gs - 1], b[200, k // gs - 1] = _SLOW_SB[dtype]
+    s[5, 0] = 0
+    b[40, 7] = 0
+    s[90, 3], b[90, 3] = 0, 0
+    s[131, 13] = s[131, 13] | 0x8000
+    b[131, 13] = 0x8000
+    x = make_x(rng, m, k, dtype)
+    y = _run(device, library, w_q, s, b, x, m, n, k, gs, 4, dtype)
+    _check(oracle, y, x, w_q, s, b, m, n, k, gs, 4, dtype, f"{form} slow/zero groups {dtype}")
