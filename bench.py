@@ -52,6 +52,7 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
+import re
 import os
 import sys
 import time
@@ -761,10 +762,17 @@ def _pmc_per_dispatch(d, counter):
     return _pmc_table(d).get(counter, {})
 
 
-def counter_summary(dirs, min_dispatches=20):
+def _short_kernel(name):
+    name = re.sub(r"\((unsigned|cpq::).*$", "", name)
+    return name.replace("void cpq::(anonymous namespace)::", "").replace("cpq::dev::", "")
+
+
+def counter_summary(dirs, min_dispatches=20, per_wave=False):
     """Markdown table of every counter of one or more --pmc runs, mean per
     dispatch, one row per (kernel, grid) seen in every run with at least
-    `min_dispatches` dispatches (the benchmark's timed kernels, not set-up)."""
+    `min_dispatches` dispatches (the benchmark's timed kernels, not set-up).
+    per_wave: the per-wave figures instead (quad-cycle counters x 4,
+    SQ_BUSY_CYCLES / 32 shader engines, MFMA busy and co-issue / 1024 SIMDs)."""
     tabs = {}
     for d in dirs:
         tabs.update(_pmc_table(d))
@@ -772,10 +780,27 @@ def counter_summary(dirs, min_dispatches=20):
     for t in tabs.values():
         ks = {k for k, (_, n) in t.items() if n >= min_dispatches}
         keys = ks if keys is None else keys & ks
+    keys = sorted(keys or (), key=lambda kk: (kk[0], kk[1]))
+    if per_wave:
+        print("| kernel | grid | waves | wave life (cyc) | busy (cyc) | VALU instr / wave | MFMA / wave | "
+              "s_waitcnt stall / wave (cyc) | VALU active / wave (cyc) | MFMA busy / SIMD (cyc) | "
+              "VALU+MFMA co-issue / SIMD (cyc) | FETCH_SIZE (KiB) | LDS bank conflicts |")
+        print("|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|")
+        for k in keys:
+            if k[0].startswith("__amd"):
+                continue
+            v = lambda c: tabs.get(c, {}).get(k, (float("nan"), 0))[0]
+            w = v("SQ_WAVES")
+            row = [w, v("SQ_WAVE_CYCLES") * 4 / w, v("SQ_BUSY_CYCLES") / 32, v("SQ_INSTS_VALU") / w,
+                   v("SQ_INSTS_MFMA") / w, v("SQ_WAIT_INST_ANY") * 4 / w, v("SQ_ACTIVE_INST_VALU") * 4 / w,
+                   v("SQ_VALU_MFMA_BUSY_CYCLES") / 1024, v("SQ_VALU_MFMA_COEXEC_CYCLES") / 1024, v("FETCH_SIZE"),
+                   v("SQ_LDS_BANK_CONFLICT")]
+            print(f"| `{_short_kernel(k[0])}` | {k[1]} | " + " | ".join(f"{x:.0f}" for x in row) + " |")
+        return
     cols = sorted(tabs)
     print("| kernel | grid | dispatches | " + " | ".join(cols) + " |")
     print("|---|---:|---:|" + "---:|" * len(cols))
-    for k in sorted(keys or (), key=lambda kk: (kk[0], kk[1])):
+    for k in keys:
         n = min(tabs[c][k][1] for c in cols)
         vals = " | ".join(f"{tabs[c][k][0]:.6g}" for c in cols)
         print(f"| `{k[0]}` | {k[1]} | {n} | {vals} |")
@@ -861,10 +886,11 @@ def main():
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"))
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_DIR")
     ap.add_argument("--counter-summary", nargs="+", metavar="PMC_DIR")
+    ap.add_argument("--per-wave", action="store_true", help="with --counter-summary: per-wave figures")
     args = ap.parse_args()
 
     if args.counter_summary:
-        counter_summary(args.counter_summary)
+        counter_summary(args.counter_summary, per_wave=args.per_wave)
         return
     if args.trace_summary:
         trace_summary(args.trace_summary)
