@@ -806,8 +806,50 @@ def counter_summary(dirs, min_dispatches=20, per_wave=False):
         print(f"| `{k[0]}` | {k[1]} | {n} | {vals} |")
 
 
-def trace_summary(d):
-    """Per (kernel, grid) durations from a rocprofv3 --kernel-trace run."""
+# The bench row each traced (kernel name fragment, launch grid in threads)
+# belongs to, for the markdown form of --trace-summary.
+TRACE_WORKLOADS = (
+    ("qmv_lean_kernel<cpq::dev::BF16, 4, 6, 4, 8, true, false>", 196608, "**cfg2a qmv** (headline)"),
+    ("qmv_lean_kernel<cpq::dev::BF16, 4, 6, 12, 8, true, false>", 196608, "cfg2b qmv"),
+    ("qmv_lean_kernel<cpq::dev::F16, 4, 6, 4, 4, true, false>", 32768, "cfg1 qmv (f16)"),
+    ("qmm_dma_kernel", 131072, "**cfg3a qmm** (headline)"),
+    ("qmm_dma_kernel", 196608, "cfg3b"),
+    ("qmm_dma_kernel", 262144, "cfg3c N=4096"),
+    ("qmm_dma_kernel", 786432, "cfg3c N=12288"),
+    ("qmm_staged_kernel<cpq::dev::BF16, 8", 65536, "8-bit prefill M=512"),
+    ("qmv_lean_kernel<cpq::dev::BF16, 4, 6, 4, 8, true, false>", 65536, "cfg4 4b gs64 M=1"),
+    ("qmv_lean_kernel<cpq::dev::BF16, 4, 5, 4, 8, true, false>", 65536, "cfg4 4b gs32 M=1"),
+    ("qmv_lean_kernel<cpq::dev::BF16, 8, 6, 4, 8, true, false>", 65536, "cfg4 8b M=1"),
+    ("qmm_lean_rows_kernel<cpq::dev::BF16, 4, 6, 8, 4, false, 16>", 131072, "cfg4 4b gs64 M=4, M=16"),
+    ("qmm_lean_rows_kernel<cpq::dev::BF16, 4, 5, 8, 4, false, 16>", 131072, "cfg4 4b gs32 M=4"),
+    ("qmm_lean_rows_kernel<cpq::dev::BF16, 4, 5, 8, 4, false, 8>", 131072, "cfg4 4b gs32 M=16"),
+    ("qmm_lean_rows_kernel<cpq::dev::BF16, 8, 6, 4, 8, false, 16>", 65536, "cfg4 8b M=4"),
+    ("qmm_lean_rows_kernel<cpq::dev::BF16, 8, 6, 8, 4, false, 16>", 131072, "cfg4 8b M=16"),
+    ("qmm_small_kernel<cpq::dev::BF16, 4, 4>", 131072, "cfg4 4b M=64 (gs64 and gs32)"),
+    ("qmm_small_kernel<cpq::dev::BF16, 8, 4>", 131072, "cfg4 8b M=64"),
+    ("gather_expert_kernel", 131072, "cfg5 prefill up / down (sorted + unsorted)"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, false>", 98304, "cfg5 decode 1 token, up"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, false>", 262144, "cfg5 decode 1 token, down"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 2, false>", 196608, "cfg5 decode 4 tokens, up"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 1, false>", 262144, "cfg5 decode 4 tokens, down"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 1, true>", 607744, "reference qmv lm_head (K=896; dense form, M=1)"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true>", 77824, "reference qmv gate/up (K=896; dense form, M=1)"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true>", 14336, "reference qmv q/o, its K-padded twin (dense form, M=1)"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true>", 2048, "reference qmv k/v, its K-padded twin (dense form, M=1)"),
+    ("qmv_kernel<cpq::dev::BF16, 4, 8, 4, false>", 28672, "reference qmv down (K=4864)"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true>", 71680, "reference M=39 q, o (K=896) and down (K=4864) (dense form)"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true>", 10240, "reference M=39 k_proj (dense form)"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 2, true>", 194560, "reference M=39 gate/up (dense form)"),
+    ("qmm_rows_kernel<cpq::dev::BF16, 4, 3>", 607744, "reference M=39 lm_head (activations in LDS)"),
+    ("stream_read_kernel<256, 8, false, false>", 1048576, "cache flush (512 MiB read) before each timed replay"),
+    ("stream_read_kernel<256, 8, false, false>", 262144, "read ceiling leg"),
+    ("stream_read_kernel<256, 4, false, false>", 256, "launch floor (one workgroup, 16 B)"),
+)
+
+
+def trace_summary(d, markdown=False):
+    """Per (kernel, grid) durations from a rocprofv3 --kernel-trace run: JSON,
+    or a markdown table with each row's bench workload (TRACE_WORKLOADS)."""
     import csv
     import glob
 
@@ -823,7 +865,17 @@ def trace_summary(d):
         v.sort()
         out.append({"kernel": name, "grid": grid, "calls": len(v), "avg_ns": sum(v) / len(v), "min_ns": v[0],
                     "median_ns": v[len(v) // 2], "max_ns": v[-1]})
-    print(json.dumps(out, indent=1))
+    if not markdown:
+        print(json.dumps(out, indent=1))
+        return
+    print("| workload | kernel | grid (threads) | calls | avg ns | median ns | min ns | max ns |")
+    print("|---|---|---:|---:|---:|---:|---:|---:|")
+    for r in out:
+        if r["calls"] < 3:
+            continue
+        lab = next((l for frag, g, l in TRACE_WORKLOADS if frag in r["kernel"] and r["grid"] == g), "")
+        print(f"| {lab} | `{_short_kernel(r['kernel'])}` | {r['grid']} | {r['calls']} | {r['avg_ns']:.0f} | "
+              f"{r['median_ns']} | {r['min_ns']} | {r['max_ns']} |")
 
 
 def pmc_summary(fetch_dir, write_dir, cfetch_dir, cwrite_dir):
@@ -885,6 +937,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"))
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_DIR")
+    ap.add_argument("--markdown", action="store_true", help="with --trace-summary: markdown table by workload")
     ap.add_argument("--counter-summary", nargs="+", metavar="PMC_DIR")
     ap.add_argument("--per-wave", action="store_true", help="with --counter-summary: per-wave figures")
     args = ap.parse_args()
@@ -893,7 +946,7 @@ def main():
         counter_summary(args.counter_summary, per_wave=args.per_wave)
         return
     if args.trace_summary:
-        trace_summary(args.trace_summary)
+        trace_summary(args.trace_summary, markdown=args.markdown)
         return
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
