@@ -506,7 +506,8 @@ __global__ __launch_bounds__(64 * WAVES) void qmv_lean_kernel(const uint32_t* __
 // (16 output columns, WAVES waves over K, each wave self-contained until the
 // final sum), but each wave stages M rows of its activation range, row r at
 // r * 256 * nsteps bytes of its region with 16-byte slot s of a step stored
-// at slot s ^ r, so the 16 A rows of one MFMA read 16 distinct slots.  Rows
+// at slot s ^ swz_key(r), so the 16 lanes one A-operand read serves together
+// hit 16 distinct slots.  Rows
 // past M are not read: their A rows only feed output rows that are never
 // stored.  NST steps per wave (K = 128 * WAVES * NST); at most 16
 // activation items per lane (M * NST <= 64).  CW: bytes of a group's
@@ -587,7 +588,7 @@ __global__ __launch_bounds__(64 * WAVES) void qmm_lean_rows_kernel(const uint32_
   for (int i = 0; i < XMAX; ++i) {
     const int rr = i / IPR, t = i % IPR;
     if (rr < rows)
-      *reinterpret_cast<u32x4*>(xw + rr * RB + 1024 * t + (lane >> 4) * 256 + (((lane & 15) ^ rr) << 4)) =
+      *reinterpret_cast<u32x4*>(xw + rr * RB + 1024 * t + (lane >> 4) * 256 + (((lane & 15) ^ swz_key(rr)) << 4)) =
           interleave_x<BITS>(xv[i]);
   }
   FastQuick fq;
@@ -632,12 +633,12 @@ __global__ __launch_bounds__(64 * WAVES) void qmm_lean_rows_kernel(const uint32_
   const bool fast = __builtin_amdgcn_ballot_w64(!ok) == 0;
 
   // 4. Stream: lane (row r, group g) reads slice i of step j at
-  //    xw + r * RB + j * 256 + ((4g + i) ^ r) * 16.
+  //    xw + r * RB + j * 256 + ((4g + i) ^ swz_key(r)) * 16.
   const unsigned char* cbase = cw + (size_t)(r * cwp + ((g * 32) >> GS_SHIFT)) * CW;
   const unsigned char* xbase = xw + r * RB;
   int xsw[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) xsw[i] = ((4 * g + i) ^ r) << 4;
+  for (int i = 0; i < 4; ++i) xsw[i] = ((4 * g + i) ^ swz_key(r)) << 4;
   const f32x4 acc =
       fast ? lean_stream<TT, BITS, GS_SHIFT, PF, ONE, true, 16, CW>(wr, voff, nsteps, cbase, xbase, buf, xsw)
            : lean_stream<TT, BITS, GS_SHIFT, PF, ONE, false, 16, CW>(wr, voff, nsteps, cbase, xbase, buf, xsw);
