@@ -210,6 +210,9 @@ __global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(
       // 8 (<= 256), PF 1 up to 8 (<= 128).
       constexpr int XP = (PF == 8 || PF == 1) ? 2 : 4;
       const int pieces = np * nb * 16;
+      // q / (16 nb) as (q * inv) >> 16: exact for every q < 783 at these
+      // divisors (q < 256 here), two VALU instead of a division.
+      const uint32_t inv = (65536u + 16u * nb - 1u) / (16u * nb);
       u32x4 xv[XP];
       int xdst[XP];
 #pragma unroll
@@ -218,7 +221,7 @@ __global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(
         if (i == 0 || 64 * i < pieces) {  // uniform
           const int q = lane + 64 * i;
           const int qc = q < pieces ? q : 0;
-          const int m = qc / (nb * 16), rem = qc - m * (nb * 16), t = rem >> 4, pc = rem & 15;
+          const int m = (int)(((uint32_t)qc * inv) >> 16), rem = qc - m * (nb * 16), t = rem >> 4, pc = rem & 15;
           const int row = rlist[p0 + m];
           const uint32_t xrow = lhs ? (uint32_t)__shfl((int)xr, row, 64) : (uint32_t)row;
           xdst[i] = q < pieces ? m * RB + t * 256 + ((pc ^ swz_key(m)) << 4) : -1;
@@ -248,14 +251,31 @@ __global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
       for (int i = 0; i < XP; ++i)
         if (xdst[i] >= 0) *reinterpret_cast<u32x4*>(xw + xdst[i]) = interleave_x<BITS>(xv[i]);
-      // 2c. Vote (within the wave) on the single-FMA dequantization.
-      bool ok = true;
-#pragma unroll
-      for (int t = 0; t < PF; ++t) ok &= !live[t] || fast_ok_bits<TT>(sv[t], bv[t]);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_wave_barrier();  // the staged slices before any lane reads them
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const bool fast = ballot(!ok) == 0;
+      // 2c. Vote (within the wave) on the single-FMA dequantization: the
+      //     packed exponent check over the batch's (scale, bias) pairs, two
+      //     per word (slots past the batch or past K count as (1, 1), which
+      //     passes), and the exact per-group check only when some lane
+      //     fails it.
+      constexpr uint32_t kOne = Sig16<TT>::bf16 ? 0x3F80u : 0x3C00u;
+      FastQuick fq;
+      fast_quick_init(fq);
+#pragma unroll
+      for (int t = 0; t < PF; t += 2) {
+        const int t1 = t + 1 < PF ? t + 1 : t;
+        const uint32_t sa = live[t] ? sv[t] : kOne, ba = live[t] ? bv[t] : kOne;
+        const uint32_t sb = live[t1] ? sv[t1] : kOne, bb = live[t1] ? bv[t1] : kOne;
+        fast_quick_add<TT>(fq, sa | (sb << 16), ba | (bb << 16));
+      }
+      bool fast = ballot(!fast_quick_ok<TT>(fq)) == 0;
+      if (!fast) {
+        bool ok = true;
+#pragma unroll
+        for (int t = 0; t < PF; ++t) ok &= !live[t] || fast_ok_bits<TT>(sv[t], bv[t]);
+        fast = ballot(!ok) == 0;
+      }
       // 2d. Multiply: A row m = lane & 15 (rows past the pass read row np-1:
       //     their outputs are never stored).
       const int m = min(r, np - 1);
