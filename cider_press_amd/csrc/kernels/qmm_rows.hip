@@ -135,6 +135,9 @@ __global__ __launch_bounds__(64 * kRowsWaves) __attribute__((amdgpu_waves_per_eu
     __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(smem + 1024 * i), 16,
                                              off, 0, 0, 0);
   }
+  // The first batch waits for the copies by count (wait_vmcnt below): no
+  // load may move above them.
+  __asm__ __volatile__("" ::: "memory");
 
   // 2. This lane's weight streams: columns n0 + 16 c + r, chunk g of each
   //    step.  Columns past N read zeros through the range check (offsets
