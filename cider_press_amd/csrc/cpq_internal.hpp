@@ -227,7 +227,7 @@ bool session_scratch(const cpq_commands* cmds, size_t bytes, void** out);
 // workgroup per (expert, column chunk); it also validates the indices (bad
 // rows zeroed, bad rows and sorted-order descents counted into *status).  gather_expert_supported says whether
 // it applies; launch_gather_qmm uses it when it does.
-bool gather_expert_supported(int bits, int n_rows, int n, int k);
+bool gather_expert_supported(int bits, int x_rows, int n_rows, int n, int k);
 hipError_t launch_gather_expert(hipStream_t s, const QuantArgs& q, const void* x, int x_rows,
                                 const uint32_t* lhs, const uint32_t* rhs, int n_rows, void* y,
                                 int n_experts, int n, int k, bool sorted, int cu_count,

@@ -57,6 +57,7 @@ struct GxShared {
   int cnt[GX_MAXBLK];  // unsorted routing: matches of this expert per 64-row block, then prefix
   int rows[64];        // routed rows of the pass (-1: none)
   int xrow[64];        // their activation rows (-1: none / invalid)
+  int orow[64];        // output row of each pass row (-1: not stored)
   int total, lo;
 };
 
@@ -229,6 +230,7 @@ struct GxCtx {
   uint32_t sel;
   uint32_t aoff[4];
   const unsigned char* xs;
+  const int* orow;  // LDS: the pass's output rows
   int col0, n;
   __amdgpu_buffer_rsrc_t yr;
 };
@@ -241,13 +243,26 @@ struct GxCtx {
 // the ones that hold rows of the pass (each block read costs LDS bandwidth).
 template <typename TT, int BITS, int MB, int MBL, bool FAST, int QS, int GSQ>
 __device__ __forceinline__ void gx_group(const GxSrc& src, GxRing<BITS, QS, GSQ>& ring, GxPos& wpos, GxPos& spos,
-                                         GxPos& cur, int t0, f32x4 (&acc)[MB], const int (&orow)[MB][4],
-                                         const GxCtx& cx) {
+                                         GxPos& cur, int t0, f32x4 (&acc)[MB], const GxCtx& cx) {
 #pragma unroll
   for (int p = 0; p < GX_UNROLL; ++p) {
     const int t = t0 + p;
     constexpr int kSbSlots = GxRing<BITS, QS, GSQ>::kSb;
     const int q = (p / QS) % kSbSlots, I = p % QS;
+    // This step's activation operands first: their LDS latency runs under
+    // the dequantization instead of between the MFMAs.
+    // (Up to two blocks: more would hold too many registers across the
+    // dequantization.)
+    constexpr bool kEarly = MBL <= 2;
+    const uint32_t ub = (uint32_t)cur.u * (MB * 4096u);
+    u32x4 a[4][MBL];
+    if constexpr (kEarly) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int mb = 0; mb < MBL; ++mb)
+          a[i][mb] = *reinterpret_cast<const u32x4*>(cx.xs + cx.aoff[i] + ub + mb * 4096);
+    }
     const float sf = gx_sbv<TT, QS, GSQ>(ring.s[q], I, cx.sel);
     const float bf = gx_sbv<TT, QS, GSQ>(ring.b[q], I, cx.sel);
     const float s16 = sf * 0.0625f;
@@ -267,29 +282,31 @@ __device__ __forceinline__ void gx_group(const GxSrc& src, GxRing<BITS, QS, GSQ>
                          ring.s[q], ring.b[q]);
       spos.skip(QS, cx.units);
     }
-    const uint32_t ub = (uint32_t)cur.u * (MB * 4096u);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const unsigned char* xa = cx.xs + cx.aoff[i] + ub;
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int mb = 0; mb < MBL; ++mb) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(xa + mb * 4096);
-        acc[mb] = Mfma16<TT>::run(a, bop[i], acc[mb]);
+        if constexpr (!kEarly) a[i][mb] = *reinterpret_cast<const u32x4*>(cx.xs + cx.aoff[i] + ub + mb * 4096);
+        acc[mb] = Mfma16<TT>::run(a[i][mb], bop[i], acc[mb]);
       }
-    }
     if (cur.u == cx.units - 1) {  // slab done (uniform)
       if (cur.j < cx.my_slabs) {
         // Rows of the pass and columns inside n store; the others take an
         // offset past the buffer, which drops the store.
         const int col = cx.col0 + 16 * GX_WAVES * cur.j;
 #pragma unroll
-        for (int mb = 0; mb < MBL; ++mb)
+        for (int mb = 0; mb < MBL; ++mb) {
+          // Rows 16 mb + 4 g + i of the pass, read from LDS here rather than
+          // held in registers through the stream.
+          const u32x4 o = *reinterpret_cast<const u32x4*>(cx.orow + 16 * mb + 4 * cx.g);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const bool ok = orow[mb][i] >= 0 && col < cx.n;
-            const uint32_t off = ok ? ((uint32_t)orow[mb][i] * (uint32_t)cx.n + (uint32_t)col) * 2u : 0x80000000u;
+            const int orw = (int)o[i];
+            const bool ok = orw >= 0 && col < cx.n;
+            const uint32_t off = ok ? ((uint32_t)orw * (uint32_t)cx.n + (uint32_t)col) * 2u : 0x80000000u;
             __builtin_amdgcn_raw_buffer_store_b16(TT::from_f32(acc[mb][i]), cx.yr, off, 0, 0);
           }
+        }
       }
 #pragma unroll
       for (int mb = 0; mb < MBL; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -302,7 +319,7 @@ __device__ __forceinline__ void gx_group(const GxSrc& src, GxRing<BITS, QS, GSQ>
 // when its (scale, bias) loads allow it.
 template <typename TT, int BITS, int MB, int MBL, int QS, int GSQ>
 __device__ __forceinline__ void gx_groups(const GxSrc& src, GxRing<BITS, QS, GSQ>& ring, GxPos wpos, GxPos spos,
-                                          const int (&orow)[MB][4], const GxCtx& cx) {
+                                          const GxCtx& cx) {
   f32x4 acc[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -314,9 +331,9 @@ __device__ __forceinline__ void gx_groups(const GxSrc& src, GxRing<BITS, QS, GSQ
 #pragma unroll
     for (int q = 0; q < GxRing<BITS, QS, GSQ>::kSb; ++q) gx_fast_add<TT, QS>(fq, ring.s[q], ring.b[q], cx.g);
     if (__builtin_amdgcn_ballot_w64(!fast_quick_ok<TT>(fq)) == 0ull)
-      gx_group<TT, BITS, MB, MBL, true, QS, GSQ>(src, ring, wpos, spos, cur, t0, acc, orow, cx);
+      gx_group<TT, BITS, MB, MBL, true, QS, GSQ>(src, ring, wpos, spos, cur, t0, acc, cx);
     else
-      gx_group<TT, BITS, MB, MBL, false, QS, GSQ>(src, ring, wpos, spos, cur, t0, acc, orow, cx);
+      gx_group<TT, BITS, MB, MBL, false, QS, GSQ>(src, ring, wpos, spos, cur, t0, acc, cx);
   }
 }
 
@@ -324,15 +341,15 @@ __device__ __forceinline__ void gx_groups(const GxSrc& src, GxRing<BITS, QS, GSQ
 // blocks that hold rows of the pass are read and multiplied).
 template <typename TT, int BITS, int MB, int QS, int GSQ>
 __device__ __forceinline__ void gx_stream(const GxSrc& src, GxRing<BITS, QS, GSQ>& ring, GxPos wpos, GxPos spos,
-                                          const int (&orow)[MB][4], const GxCtx& cx) {
+                                          const GxCtx& cx) {
   if constexpr (MB >= 4)
     if (cx.mbl >= 3) {
-      if (cx.mbl == 4) return gx_groups<TT, BITS, MB, 4, QS, GSQ>(src, ring, wpos, spos, orow, cx);
-      return gx_groups<TT, BITS, MB, 3, QS, GSQ>(src, ring, wpos, spos, orow, cx);
+      if (cx.mbl == 4) return gx_groups<TT, BITS, MB, 4, QS, GSQ>(src, ring, wpos, spos, cx);
+      return gx_groups<TT, BITS, MB, 3, QS, GSQ>(src, ring, wpos, spos, cx);
     }
   if constexpr (MB >= 2)
-    if (cx.mbl == 2) return gx_groups<TT, BITS, MB, 2, QS, GSQ>(src, ring, wpos, spos, orow, cx);
-  gx_groups<TT, BITS, MB, 1, QS, GSQ>(src, ring, wpos, spos, orow, cx);
+    if (cx.mbl == 2) return gx_groups<TT, BITS, MB, 2, QS, GSQ>(src, ring, wpos, spos, cx);
+  gx_groups<TT, BITS, MB, 1, QS, GSQ>(src, ring, wpos, spos, cx);
 }
 
 // First index i of the ascending a[0, n) with a[i] >= key (n if none), by one
@@ -533,6 +550,7 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
 #pragma unroll
   for (int i = 0; i < 4; ++i) cx.aoff[i] = (uint32_t)nl * 256u + (uint32_t)(((4 * g + i) ^ gx_key(nl)) * 16);
   cx.xs = xs;
+  cx.orow = sh.orow;
   cx.col0 = col0;
   cx.n = n;
   cx.yr = __builtin_amdgcn_make_buffer_rsrc((void*)y, 0, (int)((uint32_t)n_rows * (uint32_t)n * 2u), 0x00020000);
@@ -575,12 +593,18 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
     //    which reach only their own output rows (MFMA rows are independent),
     //    and those are not stored.
     const int kq = k >> 3;  // 16-byte items per row
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)x, 0, (int)((uint32_t)x_rows * (uint32_t)k * 2u), 0x00020000);
     const int nst = min(R, total - p0) * kq;  // <= R * K / 8
     // Rounds of GX_XITEMS items per thread (one round when that covers
     // R * K / 8); the bound is uniform, and nst > 0, so every thread runs the
     // first round and issues the weight steps in it.
     for (int base = 0; base < nst; base += GX_XITEMS * GX_THREADS) {
-      const int id0 = base + tid;
+      int id0 = base + tid;
+      // Opaque per pass: the items' indices and offsets are recomputed here
+      // instead of being hoisted out of the pass loop and held (or spilled)
+      // through the stream.
+      __asm__ __volatile__("" : "+v"(id0));
       // Item id = id0 + h * GX_THREADS is row id / kq, 16-byte piece id % kq;
       // both advance by fixed amounts per h (one division, not one per item).
       const int di = GX_THREADS / kq, dq = GX_THREADS - di * kq;
@@ -594,15 +618,16 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
         qq[h] = wrap ? q1 - kq : q1;
         ii[h] = ii[h - 1] + di + (wrap ? 1 : 0);
       }
+      // Every item is requested (no branch, so the count of loads in
+      // flight stays exact): items past the pass or of an invalid row take
+      // an offset past the buffer and read zeros.
       u32x4 v[GX_XITEMS];
 #pragma unroll
       for (int h = 0; h < GX_XITEMS; ++h) {
         const int id = id0 + h * GX_THREADS;
-        v[h] = u32x4{0u, 0u, 0u, 0u};
-        if (id < nst) {
-          const int xi = sh.xrow[ii[h]];
-          if (xi >= 0) v[h] = *reinterpret_cast<const u32x4*>(x + (size_t)xi * k + (size_t)qq[h] * 8);
-        }
+        const int xi = id < nst ? sh.xrow[min(ii[h], R - 1)] : -1;
+        const uint32_t off = xi >= 0 ? ((uint32_t)xi * (uint32_t)k + (uint32_t)qq[h] * 8u) * 2u : 0x80000000u;
+        v[h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
       }
       if (base == 0) gx_fill<BITS, QS, GSQ>(src, ring, T, units, wpos, spos);
 #pragma unroll
@@ -617,21 +642,14 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
         }
       }
     }
-    // This lane's output rows: row 16 mb + 4 g + i of the pass (-1: none).
-    int orow[MB][4];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int rl = 16 * mb + 4 * g + i;
-        orow[mb][i] = sh.rows[rl] >= 0 && sh.xrow[rl] >= 0 ? sh.rows[rl] : -1;
-      }
+    // The pass's output rows (-1: none).
+    if (tid < R) sh.orow[tid] = sh.rows[tid] >= 0 && sh.xrow[tid] >= 0 ? sh.rows[tid] : -1;
     __syncthreads();
 
     // 5. Stream the weights of this wave's slabs (again for every further
     //    pass).
     cx.mbl = (min(R, total - p0) + 15) >> 4;
-    if (T > 0) gx_stream<TT, BITS, MB, QS, GSQ>(src, ring, wpos, spos, orow, cx);
+    if (T > 0) gx_stream<TT, BITS, MB, QS, GSQ>(src, ring, wpos, spos, cx);
     __syncthreads();  // LDS rows / activations are rewritten by the next pass
   }
   check_rows();
@@ -670,7 +688,7 @@ hipError_t launch_mb(hipStream_t s, const QuantArgs& q, const void* x, int x_row
   const uintptr_t al = reinterpret_cast<uintptr_t>(q.scales) | reinterpret_cast<uintptr_t>(q.biases);
   // Buffer offsets of one expert's tables and of Y stay inside 31 bits.
   if ((uint64_t)n * k * BITS / 8 >= (1ull << 31) || (uint64_t)n * G * 2 >= (1ull << 31) ||
-      (uint64_t)n_rows * n * 2 >= (1ull << 31))
+      (uint64_t)n_rows * n * 2 >= (1ull << 31) || (uint64_t)x_rows * k * 2 >= (1ull << 31))
     return hipErrorInvalidValue;
   static const int forced = env_int("CPQ_GATHER_QS", 0);
 #define CPQ_GXQ(QS, GSQ)                                                                                  \
@@ -720,10 +738,11 @@ hipError_t launch_t(hipStream_t s, const QuantArgs& q, const void* x, int x_rows
 
 }  // namespace
 
-bool gather_expert_supported(int bits, int n_rows, int n, int k) {
-  // k % 128: whole units per staged row; one expert's weights and Y within
-  // the 31-bit buffer offsets.
+bool gather_expert_supported(int bits, int x_rows, int n_rows, int n, int k) {
+  // k % 128: whole units per staged row; X, one expert's weights and Y
+  // within the 31-bit buffer offsets.
   return (bits == 4 || bits == 8) && k % 128 == 0 && n_rows <= 64 * GX_MAXBLK &&
+         (uint64_t)x_rows * k * 2 < (1ull << 31) &&
          (size_t)16 * k * 2 <= (size_t)GX_XBYTES && (uint64_t)n * k * bits / 8 < (1ull << 31) &&
          (uint64_t)n_rows * n * 2 < (1ull << 31);
 }

@@ -522,7 +522,7 @@ hipError_t launch_gather_t(hipStream_t s, const QuantArgs& q, const void* x, int
   // Few rows (decode): one pass per distinct expert (validates the indices itself).
   if (gather_decode_supported(q, x_rows, n_rows, n, k))
     return launch_gather_decode(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
-  if (gather_expert_supported(BITS, n_rows, n, k)) {  // validates the indices itself
+  if (gather_expert_supported(BITS, x_rows, n_rows, n, k)) {  // validates the indices itself
     static const int cus = [] {
       int dev = 0, cu = 0;
       if (hipGetDevice(&dev) != hipSuccess ||
@@ -580,7 +580,7 @@ bool skinny_fits(int k, int gs) {
 bool gather_supported(int bits, int n_rows, int n, int k, int gs) {
   const QuantArgs shape{nullptr, nullptr, nullptr, gs, bits, CPQ_DTYPE_BF16};
   return gather_decode_supported(shape, 1, n_rows, n, k) ||
-         gather_expert_supported(bits, n_rows, n, k) ||
+         gather_expert_supported(bits, 1, n_rows, n, k) ||
          (gs > 0 && slab_consts_bytes(k, gs) + sizeof(TileShared<4, kMaxMB>) <= (size_t)160 * 1024);
 }
 
