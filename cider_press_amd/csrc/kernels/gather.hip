@@ -57,7 +57,7 @@ struct GxShared {
   int cnt[GX_MAXBLK];  // unsorted routing: matches of this expert per 64-row block, then prefix
   int rows[64];        // routed rows of the pass (-1: none)
   int xrow[64];        // their activation rows (-1: none / invalid)
-  int orow[64];        // output row of each pass row (-1: not stored)
+  uint32_t orow[64];   // byte offset of each pass row's output row in Y (past Y: not stored)
   int total, lo;
 };
 
@@ -230,7 +230,7 @@ struct GxCtx {
   uint32_t sel;
   uint32_t aoff[4];
   const unsigned char* xs;
-  const int* orow;  // LDS: the pass's output rows
+  const uint32_t* orow;  // LDS: byte offsets of the pass's output rows
   int col0, n;
   __amdgpu_buffer_rsrc_t yr;
 };
@@ -292,8 +292,10 @@ __device__ __forceinline__ void gx_group(const GxSrc& src, GxRing<BITS, QS, GSQ>
     if (cur.u == cx.units - 1) {  // slab done (uniform)
       if (cur.j < cx.my_slabs) {
         // Rows of the pass and columns inside n store; the others take an
-        // offset past the buffer, which drops the store.
+        // offset past the buffer (rows without output: 2^31 plus the
+        // column's bytes, still below 2^32), which drops the store.
         const int col = cx.col0 + 16 * GX_WAVES * cur.j;
+        const bool colok = col < cx.n;
 #pragma unroll
         for (int mb = 0; mb < MBL; ++mb) {
           // Rows 16 mb + 4 g + i of the pass, read from LDS here rather than
@@ -301,9 +303,7 @@ __device__ __forceinline__ void gx_group(const GxSrc& src, GxRing<BITS, QS, GSQ>
           const u32x4 o = *reinterpret_cast<const u32x4*>(cx.orow + 16 * mb + 4 * cx.g);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int orw = (int)o[i];
-            const bool ok = orw >= 0 && col < cx.n;
-            const uint32_t off = ok ? ((uint32_t)orw * (uint32_t)cx.n + (uint32_t)col) * 2u : 0x80000000u;
+            const uint32_t off = colok ? o[i] + (uint32_t)col * 2u : 0x80000000u;
             __builtin_amdgcn_raw_buffer_store_b16(TT::from_f32(acc[mb][i]), cx.yr, off, 0, 0);
           }
         }
@@ -642,8 +642,9 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
         }
       }
     }
-    // The pass's output rows (-1: none).
-    if (tid < R) sh.orow[tid] = sh.rows[tid] >= 0 && sh.xrow[tid] >= 0 ? sh.rows[tid] : -1;
+    // The pass's output rows, as byte offsets into Y (2^31: none).
+    if (tid < R)
+      sh.orow[tid] = sh.rows[tid] >= 0 && sh.xrow[tid] >= 0 ? (uint32_t)sh.rows[tid] * (uint32_t)n * 2u : 0x80000000u;
     __syncthreads();
 
     // 5. Stream the weights of this wave's slabs (again for every further
