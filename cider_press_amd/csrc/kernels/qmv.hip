@@ -311,36 +311,41 @@ __device__ __forceinline__ f32x4 lean_stream(__amdgpu_buffer_rsrc_t wr, uint32_t
   constexpr int STEP_C = (128 >> GS_SHIFT) * CW;  // constants bytes per step
   constexpr int STEP_X = 4 * 64;           // activation bytes per step (4 chunks x 32 x 2 B)
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  auto step = [&](const uint32_t* cur, int j) {
+  // ONE: a step's LDS operands (its group constants and four activation
+  // slices) are read one step ahead, so their latency runs under the
+  // previous step's dequantization instead of in front of this one's (the
+  // looped form keeps them in the step: the look-ahead's registers would
+  // spill there).
+  using CV = std::conditional_t<CW == 16, f32x4, f32x2>;
+  struct Ops {
+    CV gc;
+    u32x4 a[4];
+  };
+  auto load_ops = [&](int j, Ops& o) {
+    o.gc = *reinterpret_cast<const CV*>(cbase + j * STEP_C);
+    const unsigned char* xj = xbase + j * STEP_X;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o.a[i] = *reinterpret_cast<const u32x4*>(xj + (MR == 1 ? 16 * i : xsw[i]));
+  };
+  auto step = [&](const uint32_t* cur, const Ops& o) {
     float sc, b, c0, c1;
+    sc = o.gc[0];
+    b = o.gc[1];
     if constexpr (CW == 16) {
-      const f32x4 gc = *reinterpret_cast<const f32x4*>(cbase + j * STEP_C);
-      sc = gc[0]; b = gc[1]; c0 = gc[2]; c1 = gc[3];
+      c0 = o.gc[2];
+      c1 = o.gc[3];
     } else {
-      const f32x2 gc = *reinterpret_cast<const f32x2*>(cbase + j * STEP_C);
-      sc = gc[0]; b = gc[1];
       c0 = FAST ? fmaf(-1024.f, sc, b) : 0.f;
       c1 = FAST ? fmaf(-64.f, sc, b) : 0.f;
     }
     const float s16 = sc * 0.0625f;
-    if constexpr (MR == 1) {
-      const u32x4* xa = reinterpret_cast<const u32x4*>(xbase + j * STEP_X);
-      acc = Mfma16<TT>::run(xa[0], dequant_slice<TT, BITS, FAST, 0>(cur, sc, s16, b, c0, c1), acc);
-      acc = Mfma16<TT>::run(xa[1], dequant_slice<TT, BITS, FAST, 1>(cur, sc, s16, b, c0, c1), acc);
-      acc = Mfma16<TT>::run(xa[2], dequant_slice<TT, BITS, FAST, 2>(cur, sc, s16, b, c0, c1), acc);
-      acc = Mfma16<TT>::run(xa[3], dequant_slice<TT, BITS, FAST, 3>(cur, sc, s16, b, c0, c1), acc);
-    } else {
-      const unsigned char* xj = xbase + j * STEP_X;
-      const u32x4 a0 = *reinterpret_cast<const u32x4*>(xj + xsw[0]);
-      const u32x4 a1 = *reinterpret_cast<const u32x4*>(xj + xsw[1]);
-      const u32x4 a2 = *reinterpret_cast<const u32x4*>(xj + xsw[2]);
-      const u32x4 a3 = *reinterpret_cast<const u32x4*>(xj + xsw[3]);
-      acc = Mfma16<TT>::run(a0, dequant_slice<TT, BITS, FAST, 0>(cur, sc, s16, b, c0, c1), acc);
-      acc = Mfma16<TT>::run(a1, dequant_slice<TT, BITS, FAST, 1>(cur, sc, s16, b, c0, c1), acc);
-      acc = Mfma16<TT>::run(a2, dequant_slice<TT, BITS, FAST, 2>(cur, sc, s16, b, c0, c1), acc);
-      acc = Mfma16<TT>::run(a3, dequant_slice<TT, BITS, FAST, 3>(cur, sc, s16, b, c0, c1), acc);
-    }
+    acc = Mfma16<TT>::run(o.a[0], dequant_slice<TT, BITS, FAST, 0>(cur, sc, s16, b, c0, c1), acc);
+    acc = Mfma16<TT>::run(o.a[1], dequant_slice<TT, BITS, FAST, 1>(cur, sc, s16, b, c0, c1), acc);
+    acc = Mfma16<TT>::run(o.a[2], dequant_slice<TT, BITS, FAST, 2>(cur, sc, s16, b, c0, c1), acc);
+    acc = Mfma16<TT>::run(o.a[3], dequant_slice<TT, BITS, FAST, 3>(cur, sc, s16, b, c0, c1), acc);
   };
+  Ops ops;
   int base = 0;
   // ONE: the whole range is the PF prefetched steps (no loop, buffers consumed in place).
   for (; !ONE && base + PF < nsteps; base += PF) {
@@ -351,11 +356,26 @@ __device__ __forceinline__ f32x4 lean_stream(__amdgpu_buffer_rsrc_t wr, uint32_t
 #pragma unroll
       for (int i = 0; i < BITS; ++i) cur[i] = buf[p][i];
       lean_load<BITS>(wr, voff + p * STEP_W, soff, buf[p]);
-      step(cur, base + p);
+      load_ops(base + p, ops);
+      step(cur, ops);
     }
   }
+  if constexpr (ONE) {
+    Ops ops, nxt;
+    load_ops(0, ops);
 #pragma unroll
-  for (int p = 0; p < PF; ++p) step(buf[p], base + p);
+    for (int p = 0; p < PF; ++p) {
+      if (p + 1 < PF) load_ops(p + 1, nxt);
+      step(buf[p], ops);
+      ops = nxt;
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      load_ops(base + p, ops);
+      step(buf[p], ops);
+    }
+  }
   return acc;
 }
 
