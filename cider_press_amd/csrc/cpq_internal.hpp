@@ -236,7 +236,7 @@ hipError_t launch_gather_expert(hipStream_t s, const QuantArgs& q, const void* x
 // Routed experts at decode shapes (kernels/gather_decode.hip): up to 64
 // rows, 4/8-bit, K % 128 == 0; one workgroup per (distinct expert, 16
 // columns); validates the indices itself.
-int gather_decode_kw(int slots, int n, int k);
+int gather_decode_kw(int slots, int n, int k, bool dense);
 size_t gather_decode_lds(int rows_max, int k, int kw);
 // The same kernel as a small-M matmul (rows in passes of 8, one workgroup
 // per (column group, pass)): 1 <= M <= 64, 4/8-bit, K a multiple of the

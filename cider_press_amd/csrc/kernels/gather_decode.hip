@@ -356,7 +356,7 @@ hipError_t launch_dec_w(hipStream_t s, const QuantArgs& q, const void* x, int x_
                         const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
                         unsigned int* status, bool pad_exact) {
   const int slots = DENSE ? (n_rows + kDensePass - 1) / kDensePass : n_rows;
-  int kw = gather_decode_kw(slots, n, k);
+  int kw = gather_decode_kw(slots, n, k, DENSE);
   if (pad_exact && kw == 2) kw = 4;
   if (kw == 4)
     return launch_dec<TT, BITS, 4, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
@@ -386,22 +386,32 @@ hipError_t launch_dec_any(hipStream_t s, const QuantArgs& q, const void* x, int 
 
 }  // namespace
 
-// Waves of a workgroup splitting K (the other factor of 4 splits columns):
-// the most that keep the grid (column blocks x slots) within what the CUs
-// hold at once, about 4 workgroups each, since every workgroup pays the same
-// chain of dependent round trips (routing, weights and activations, sum);
-// with a longer K fewer column blocks per workgroup keep more loads in
-// flight per CU.
-int gather_decode_kw(int n_rows, int n, int k) {
+// Waves of a workgroup splitting K (the other factor of 4 splits columns),
+// among the splits that keep the grid (column blocks x slots) within what
+// the CUs hold at once, about 4 workgroups each, since every workgroup pays
+// the same chain of dependent round trips (routing, weights and activations,
+// sum).  The dense form takes the most such waves (its padded and unpadded
+// K must choose alike); the routed form the split with the fewest steps per
+// wave plus one per part (each part adds a share of the LDS sum and a wave
+// that may be left short): config 5's down projection at one token (6
+// steps) runs 5.47 us with 2 parts against 5.79 with 4.
+int gather_decode_kw(int n_rows, int n, int k, bool dense) {
   const int forced = env_int("CPQ_DEC_KW", 0);  // tuning hook: 1, 2 or 4
   if (forced == 1 || forced == 2 || forced == 4) return forced;
   const long blocks = (n + 15) / 16;
+  const int S = (k + 127) / 128;
+  int best = 1, best_cost = S + 1;
   for (int kw = 4; kw > 1; kw /= 2) {
     const long wgs = (long)n_rows * ((blocks + (4 / kw) - 1) / (4 / kw));
-    if (wgs <= 1024) return kw;
+    if (wgs > 1024) continue;
+    if (dense) return kw;
+    const int cost = (S + kw - 1) / kw + kw;
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = kw;
+    }
   }
-  (void)k;
-  return 1;
+  return best;
 }
 
 size_t gather_decode_lds(int rows_max, int k, int kw) {
@@ -419,7 +429,7 @@ bool gather_decode_supported(const QuantArgs& q, int x_rows, int n_rows, int n, 
   if (k % 128 != 0 || k < 128) return false;
   if ((uint64_t)n * (uint64_t)k * q.bits / 8 >= (1ull << 31) - (1ull << 20)) return false;
   if ((uint64_t)n * (uint64_t)(k / q.gs) * 2 >= (1ull << 31)) return false;
-  return gather_decode_lds(std::min(kDecPass, n_rows), k, gather_decode_kw(n_rows, n, k)) <=
+  return gather_decode_lds(std::min(kDecPass, n_rows), k, gather_decode_kw(n_rows, n, k, false)) <=
          (size_t)160 * 1024 - 1024;
 }
 
@@ -438,7 +448,7 @@ bool dense_small_supported(const QuantArgs& q, int m, int n, int k) {
   if ((uint64_t)n * (uint64_t)k * q.bits / 8 >= (1ull << 31) - (1ull << 20)) return false;
   if ((uint64_t)n * (uint64_t)(k / q.gs) * 2 >= (1ull << 31)) return false;
   const int slots = (m + kDensePass - 1) / kDensePass;
-  return gather_decode_lds(std::min(kDensePass, m), k, gather_decode_kw(slots, n, k)) <= (size_t)160 * 1024 - 1024;
+  return gather_decode_lds(std::min(kDensePass, m), k, gather_decode_kw(slots, n, k, true)) <= (size_t)160 * 1024 - 1024;
 }
 
 hipError_t launch_dense_small(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k,
