@@ -379,6 +379,17 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also
+// waits for every global load and store the wave has in flight (on gfx9
+// the vector-memory counter covers both); this one waits for the wave's
+// LDS operations, so prefetched operands and stores stay in flight across
+// it.  Use it where the barrier protects LDS data alone.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Wave64 sum via DPP-friendly butterfly.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

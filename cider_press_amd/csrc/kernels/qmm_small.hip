@@ -181,8 +181,12 @@ __global__ __launch_bounds__(512) void qmm_small_kernel(const uint32_t* __restri
         if (i < ncopies && (64 * i) / RU < rows) *reinterpret_cast<u32x4*>(smem + 1024 * i + 16 * lane) = xv[j];
       }
     }
-    wait_vmcnt<0>();
-    __syncthreads();
+    // The barrier waits for the LDS writes only: a unit's weights are
+    // waited for where the unit starts, so the first units compute while
+    // the later ones are still arriving (M = 64 at N = K = 4096: 13.1 ->
+    // 12.5 us).  Copies into LDS count as loads, so they are waited for.
+    if (xdma) wait_vmcnt<0>();
+    lds_barrier();
 
     // 3. Dequantize and multiply; the next step's A operands are read while
     //    a step is dequantized.
