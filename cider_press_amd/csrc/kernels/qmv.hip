@@ -302,10 +302,20 @@ __host__ __device__ constexpr size_t lean_wave_lds(int nsteps, int gs_shift, int
 // xbase + xsw[i] + j * STEP_X (per-lane swizzled offsets of its row).
 // CW: bytes per group's constants, 16 (s, b, b - 1024 s, b - 64 s) or 8
 // (s, b; the other two computed per step, the same fmaf).
-template <typename TT, int BITS, int GS_SHIFT, int PF, bool ONE, bool FAST, int MR = 1, int CW = 16>
+struct NoStage {
+  __device__ void operator()(int) const {}
+};
+
+// stage(j), where given, writes step j's activation slices into LDS (and
+// orders them within the wave) right before the step's operands are read:
+// the fully unrolled form then waits for each step's activations as it
+// reaches them.
+template <typename TT, int BITS, int GS_SHIFT, int PF, bool ONE, bool FAST, int MR = 1, int CW = 16,
+          typename Stage = NoStage>
 __device__ __forceinline__ f32x4 lean_stream(__amdgpu_buffer_rsrc_t wr, uint32_t voff, int nsteps,
                                              const unsigned char* cbase, const unsigned char* xbase,
-                                             uint32_t (&buf)[PF][BITS], const int* xsw = nullptr) {
+                                             uint32_t (&buf)[PF][BITS], const int* xsw = nullptr,
+                                             Stage stage = Stage{}) {
   constexpr int CB = BITS * 4;             // bytes per 32-element chunk
   constexpr int STEP_W = 4 * CB;           // weight bytes a lane group advances per step
   constexpr int STEP_C = (128 >> GS_SHIFT) * CW;  // constants bytes per step
@@ -362,10 +372,14 @@ __device__ __forceinline__ f32x4 lean_stream(__amdgpu_buffer_rsrc_t wr, uint32_t
   }
   if constexpr (ONE) {
     Ops ops, nxt;
+    stage(0);
     load_ops(0, ops);
 #pragma unroll
     for (int p = 0; p < PF; ++p) {
-      if (p + 1 < PF) load_ops(p + 1, nxt);
+      if (p + 1 < PF) {
+        stage(p + 1);
+        load_ops(p + 1, nxt);
+      }
       step(buf[p], ops);
       ops = nxt;
     }
@@ -573,9 +587,8 @@ __global__ __launch_bounds__(64 * WAVES) void qmm_lean_rows_kernel(const uint32_
   const __amdgpu_buffer_rsrc_t xr =
       __builtin_amdgcn_make_buffer_rsrc((void*)x, 0, (int)((uint32_t)m * (uint32_t)k * 2u), 0x00020000);
 
-  // 1. Small loads first: this wave's scale / bias quads, then its
-  //    activation items (row rr, item t: bytes 1024 t + 16 lane of the row's
-  //    range).
+  // 1. Small loads first: this wave's scale / bias quads; then the
+  //    activation items and the weights (2).
   const int cr = lane >> 2;
   const uint32_t coff = ((uint32_t)(n0 + cr) * (uint32_t)G + (uint32_t)(u0 * GPS + 4 * (lane & 3))) * 2u;
   u32x2 sv[kLeanQuads], bv[kLeanQuads];
@@ -587,30 +600,56 @@ __global__ __launch_bounds__(64 * WAVES) void qmm_lean_rows_kernel(const uint32_
       bv[t] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(br, coff + 32u * t, 0, 0));
     }
   }
-  const uint32_t xoff = (uint32_t)u0 * 256u + (uint32_t)lane * 16u;
-  u32x4 xv[XMAX];
-#pragma unroll
-  for (int i = 0; i < XMAX; ++i) {
-    const int rr = i / IPR, t = i % IPR;
-    if (rr < rows)
-      xv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            xr, xoff + 1024u * t, (int)((uint32_t)rr * (uint32_t)k * 2u), 0));
-  }
-
-  // 2. The weight stream.
+  // 2. Activations and weights.  8-bit weights with all steps in flight
+  //    (IL): step j's activation items (item q: rows 4q + lane / 16, the
+  //    step's 16-byte slot lane % 16) and then its weights, step by step, so
+  //    the first weight steps are requested after a quarter of the
+  //    activation loads instead of after all of them, and the stream waits
+  //    for each step's data as it reaches the step (loads complete in
+  //    order); a step's items are staged right before its operands are read
+  //    (M = 4 / 16 at N = K = 4096: 6.2 -> 5.8 / 8.05 -> 7.7 us; the same
+  //    order made 4-bit weights, half the bytes per step, slower: 6.1 ->
+  //    6.8 us at M = 16).  Otherwise every activation item (row rr, item t:
+  //    bytes 1024 t + 16 lane of the row's range), then the first PF weight
+  //    steps, then the staging.
+  constexpr bool IL = ONE && BITS == 8;
   const uint32_t voff = (uint32_t)(n0 + r) * rowbytes + (uint32_t)(4 * u0 + g) * CB;
   uint32_t buf[PF][BITS];
+  u32x4 xv[XMAX];
+  constexpr int QR = XMAX / NST;  // IL: items per step (rows <= 4 QR)
+  if constexpr (IL) {
+    const uint32_t xlo =
+        (uint32_t)(lane >> 4) * (uint32_t)k * 2u + (uint32_t)u0 * 256u + (uint32_t)(lane & 15) * 16u;
 #pragma unroll
-  for (int p = 0; p < PF; ++p) lean_load<BITS>(wr, voff + p * 4 * CB, 0, buf[p]);
-
-  // 3. Stage this wave's activations and constants, vote within the wave.
+    for (int j = 0; j < NST; ++j) {
 #pragma unroll
-  for (int i = 0; i < XMAX; ++i) {
-    const int rr = i / IPR, t = i % IPR;
-    if (rr < rows)
-      *reinterpret_cast<u32x4*>(xw + rr * RB + 1024 * t + (lane >> 4) * 256 + (((lane & 15) ^ swz_key(rr)) << 4)) =
-          interleave_x<BITS>(xv[i]);
+      for (int q = 0; q < QR; ++q)
+        if (4 * q < rows)
+          xv[j * QR + q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         xr, xlo + 256u * j, (int)((uint32_t)(4 * q) * (uint32_t)k * 2u), 0));
+      lean_load<BITS>(wr, voff + j * 4 * CB, 0, buf[j]);
+    }
+  } else {
+    const uint32_t xoff = (uint32_t)u0 * 256u + (uint32_t)lane * 16u;
+#pragma unroll
+    for (int i = 0; i < XMAX; ++i) {
+      const int rr = i / IPR, t = i % IPR;
+      if (rr < rows)
+        xv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              xr, xoff + 1024u * t, (int)((uint32_t)rr * (uint32_t)k * 2u), 0));
+    }
+#pragma unroll
+    for (int p = 0; p < PF; ++p) lean_load<BITS>(wr, voff + p * 4 * CB, 0, buf[p]);
+#pragma unroll
+    for (int i = 0; i < XMAX; ++i) {
+      const int rr = i / IPR, t = i % IPR;
+      if (rr < rows)
+        *reinterpret_cast<u32x4*>(xw + rr * RB + 1024 * t + (lane >> 4) * 256 + (((lane & 15) ^ swz_key(rr)) << 4)) =
+            interleave_x<BITS>(xv[i]);
+    }
   }
+
+  // 3. Stage this wave's constants, vote within the wave.
   FastQuick fq;
   fast_quick_init(fq);
   const int cwp = GW + 1;
@@ -659,9 +698,24 @@ __global__ __launch_bounds__(64 * WAVES) void qmm_lean_rows_kernel(const uint32_
   int xsw[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) xsw[i] = ((4 * g + i) ^ swz_key(r)) << 4;
+  // IL: step j's activation items into its slots of rows 4q + lane / 16.
+  auto stage = [&](int j) {
+    if constexpr (IL) {
+#pragma unroll
+      for (int q = 0; q < QR; ++q) {
+        const int rr = 4 * q + (lane >> 4);
+        if (4 * q < rows && rr < rows)
+          *reinterpret_cast<u32x4*>(xw + rr * RB + 256 * j + (((lane & 15) ^ swz_key(rr)) << 4)) =
+              interleave_x<BITS>(xv[j * QR + q]);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  };
   const f32x4 acc =
-      fast ? lean_stream<TT, BITS, GS_SHIFT, PF, ONE, true, 16, CW>(wr, voff, nsteps, cbase, xbase, buf, xsw)
-           : lean_stream<TT, BITS, GS_SHIFT, PF, ONE, false, 16, CW>(wr, voff, nsteps, cbase, xbase, buf, xsw);
+      fast ? lean_stream<TT, BITS, GS_SHIFT, PF, ONE, true, 16, CW>(wr, voff, nsteps, cbase, xbase, buf, xsw, stage)
+           : lean_stream<TT, BITS, GS_SHIFT, PF, ONE, false, 16, CW>(wr, voff, nsteps, cbase, xbase, buf, xsw, stage);
 
   // 5. The waves' K ranges in order; element i of lane (r, g) is output row
   //    4g + i, column n0 + r.

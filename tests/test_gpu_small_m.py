@@ -118,6 +118,7 @@ def test_small_m_interleaved_shapes_keep_counters_clean(device, oracle):
     (15, 2048, 4096, 8, 32, "f16"),
     (8, 4096, 4096, 8, 32, "bf16"),     # 8-bit, K = 4096, up to 8 rows: 4 waves of 8 steps
     (3, 2080, 4096, 8, 64, "f16"),      # the same, N not a multiple of 64
+    (5, 4096, 4096, 8, 64, "bf16"),     # 8-bit, steps staged one at a time: a partial 4-row item, exact path
 ])
 def test_decode_layout_rows_parity(device, oracle, m, n, k, bits, gs, dtype):
     """Up to 16 rows on the decode kernel's layout (K of 4096, 8192 or 16384):
@@ -126,7 +127,7 @@ def test_decode_layout_rows_parity(device, oracle, m, n, k, bits, gs, dtype):
     bias) pairs (the four-float form does not fit in LDS)."""
     rng = np.random.default_rng(m * 17 + n + k)
     w_q, s, b = make_weight(rng, n, k, gs, bits, dtype)
-    if bits == 4 and (gs == 64 or m == 16):
+    if (bits == 4 and (gs == 64 or m == 16)) or (bits == 8 and m == 5):
         s[:, ::7] = 0  # zero scales: the per-group exact path inside one wave
     x = make_x(rng, m, k, dtype)
     print(f"decode rows m={m} n={n} k={k} bits={bits} gs={gs} {dtype}", flush=True)
