@@ -829,7 +829,7 @@ TRACE_WORKLOADS = (
     ("qmm_small_kernel<cpq::dev::BF16, 8, 4>", 131072, "cfg4 8b M=64"),
     ("gather_expert_kernel", 131072, "cfg5 prefill up / down (sorted + unsorted)"),
     ("gather_decode_kernel<cpq::dev::BF16, 4, 4, false>", 98304, "cfg5 decode 1 token, up"),
-    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, false>", 262144, "cfg5 decode 1 token, down"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 2, false>", 131072, "cfg5 decode 1 token, down"),
     ("gather_decode_kernel<cpq::dev::BF16, 4, 2, false>", 196608, "cfg5 decode 4 tokens, up"),
     ("gather_decode_kernel<cpq::dev::BF16, 4, 1, false>", 262144, "cfg5 decode 4 tokens, down"),
     ("gather_decode_kernel<cpq::dev::BF16, 4, 1, true>", 607744, "reference qmv lm_head (K=896; dense form, M=1)"),
