@@ -51,10 +51,12 @@ constexpr int GX_UNROLL = 8;               // steps per loop iteration: two turn
 constexpr int GX_XBYTES = 128 * 1024;      // LDS for the staged activation rows
 constexpr int GX_MAXBLK = 1024;            // 64-row routing blocks (n_rows <= 65536)
 constexpr int GX_COUNT_ROWS = 16 * GX_THREADS;  // sorted routing: counted in one pass up to this many rows
+constexpr int GX_KEEP = 4;  // unsorted routing: 64-row blocks per wave counted in one round (2048 rows)
 constexpr int GX_XITEMS = GX_XBYTES / 16 / GX_THREADS;  // staged 16-byte items per thread: all of a pass
 
 struct GxShared {
   int cnt[GX_MAXBLK];  // unsorted routing: matches of this expert per 64-row block, then prefix
+  unsigned long long keep[GX_WAVES][GX_KEEP];  // unsorted routing: match masks of each wave's first blocks
   int rows[64];        // routed rows of the pass (-1: none)
   int xrow[64];        // their activation rows (-1: none / invalid)
   uint32_t orow[64];   // byte offset of each pass row's output row in Y (past Y: not stored)
@@ -513,7 +515,27 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
       }
     }
   } else {
-    for (int b = wave; b < nblk; b += GX_WAVES) {
+    // The first GX_KEEP blocks of each wave in one round of loads, their
+    // match masks kept in LDS for the placement below, which then needs no
+    // second load of rhs (kept in registers through the stream, they cost
+    // the sorted routing 0.2-0.7 us); further blocks (past GX_KEEP * 512
+    // rows) one at a time.
+    uint32_t ev[GX_KEEP];
+#pragma unroll
+    for (int j = 0; j < GX_KEEP; ++j) {
+      const int r = ((wave + GX_WAVES * j) << 6) + lane;
+      ev[j] = r < n_rows ? rhs[r] : 0xffffffffu;
+    }
+#pragma unroll
+    for (int j = 0; j < GX_KEEP; ++j) {
+      const unsigned long long mk = __ballot(ev[j] == e);
+      const int b = wave + GX_WAVES * j;
+      if (lane == 0) {
+        sh.keep[wave][j] = mk;
+        if (b < nblk) sh.cnt[b] = __popcll(mk);
+      }
+    }
+    for (int b = wave + GX_WAVES * GX_KEEP; b < nblk; b += GX_WAVES) {
       const int r = (b << 6) + lane;
       const unsigned long long mask = __ballot(r < n_rows && rhs[r] == e);
       if (lane == 0) sh.cnt[b] = __popcll(mask);
@@ -562,15 +584,25 @@ __global__ __launch_bounds__(GX_THREADS) void gather_expert_kernel(
     if (sorted) {
       if (tid < R && p0 + tid < total) sh.rows[tid] = sh.lo + p0 + tid;
     } else {
-      for (int b = wave; b < nblk; b += GX_WAVES) {
+      // Block b's matches, ranked within the expert: its count prefix plus
+      // the matches below this lane.
+      auto place = [&](int b, unsigned long long mask) {
         const int base = sh.cnt[b];
         const int next = b + 1 < nblk ? sh.cnt[b + 1] : total;
-        if (next <= p0 || base >= p0 + R) continue;  // uniform per wave
+        if (next <= p0 || base >= p0 + R) return;  // uniform per wave
         const int r = (b << 6) + lane;
-        const bool match = r < n_rows && rhs[r] == e;
-        const unsigned long long mask = __ballot(match);
+        const bool match = (mask >> lane) & 1ull;
         const int rank = base + __popcll(mask & ((1ull << lane) - 1ull));
         if (match && rank >= p0 && rank < p0 + R) sh.rows[rank - p0] = r;
+      };
+#pragma unroll
+      for (int j = 0; j < GX_KEEP; ++j) {
+        const int b = wave + GX_WAVES * j;
+        if (b < nblk) place(b, sh.keep[wave][j]);
+      }
+      for (int b = wave + GX_WAVES * GX_KEEP; b < nblk; b += GX_WAVES) {
+        const int r = (b << 6) + lane;
+        place(b, __ballot(r < n_rows && rhs[r] == e));
       }
     }
     __syncthreads();
