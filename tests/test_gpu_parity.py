@@ -515,6 +515,23 @@ def test_gather_expert_kernel_passes(device, library, oracle, bits, k, dtype):
     assert_tol(oracle, y, ref, x, k, dtype, f"gather expert {bits}b K={k}")
 
 
+def test_gather_unsorted_past_kept_blocks(device, library, oracle):
+    """Unsorted routing over 3000 rows (47 blocks of 64): each wave counts
+    its first four blocks in one round and keeps their match masks, the
+    blocks past 2048 rows take the one-block-at-a-time path; experts with
+    many 64-row passes place their rows from both."""
+    rng = np.random.default_rng(47)
+    e, n, k, gs, rows, xr = 3, 48, 256, 64, 3000, 64
+    w_q, s, b = _experts(rng, e, n, k, gs, 4, "bf16")
+    x = make_x(rng, xr, k, "bf16")
+    rhs = rng.integers(0, e, size=rows).astype(np.uint32)
+    rhs[2500:] = 1  # the tail blocks: one expert only
+    lhs = rng.integers(0, xr, size=rows).astype(np.uint32)
+    y = run_gather(device, library, x, w_q, s, b, lhs, rhs, rows, n, k, e, gs, 4, "bf16", False)
+    ref = oracle.gather_qmm_ref(x, lhs, rhs, w_q, s, b, rows, n, k, gs, 4, "bf16")
+    assert_tol(oracle, y, ref, x, k, "bf16", "gather unsorted 3000 rows")
+
+
 @pytest.mark.parametrize("gs,k,dtype,bits,n", [
     (64, 768, "bf16", 4, 512),     # 6 units per slab: scale / bias pairs of steps (8-byte loads)
     (64, 768, "f16", 4, 512),
