@@ -828,18 +828,18 @@ TRACE_WORKLOADS = (
     ("qmm_small_kernel<cpq::dev::BF16, 4, 4>", 131072, "cfg4 4b M=64 (gs64 and gs32)"),
     ("qmm_small_kernel<cpq::dev::BF16, 8, 4>", 131072, "cfg4 8b M=64"),
     ("gather_expert_kernel", 131072, "cfg5 prefill up / down (sorted + unsorted)"),
-    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, false>", 98304, "cfg5 decode 1 token, up"),
-    ("gather_decode_kernel<cpq::dev::BF16, 4, 2, false>", 131072, "cfg5 decode 1 token, down"),
-    ("gather_decode_kernel<cpq::dev::BF16, 4, 2, false>", 196608, "cfg5 decode 4 tokens, up"),
-    ("gather_decode_kernel<cpq::dev::BF16, 4, 1, false>", 262144, "cfg5 decode 4 tokens, down"),
-    ("gather_decode_kernel<cpq::dev::BF16, 4, 1, true>", 607744, "reference qmv lm_head (K=896; dense form, M=1)"),
-    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true>", 77824, "reference qmv gate/up (K=896; dense form, M=1)"),
-    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true>", 14336, "reference qmv q/o, its K-padded twin (dense form, M=1)"),
-    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true>", 2048, "reference qmv k/v, its K-padded twin (dense form, M=1)"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, false, true>", 98304, "cfg5 decode 1 token, up"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 2, false, true>", 131072, "cfg5 decode 1 token, down"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 2, false, true>", 196608, "cfg5 decode 4 tokens, up"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 1, false, true>", 262144, "cfg5 decode 4 tokens, down"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 1, true, true>", 607744, "reference qmv lm_head (K=896; dense form, M=1)"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true, true>", 77824, "reference qmv gate/up (K=896; dense form, M=1)"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true, true>", 14336, "reference qmv q/o, its K-padded twin (dense form, M=1)"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true, true>", 2048, "reference qmv k/v, its K-padded twin (dense form, M=1)"),
     ("qmv_kernel<cpq::dev::BF16, 4, 8, 4, false>", 28672, "reference qmv down (K=4864)"),
-    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true>", 71680, "reference M=39 q, o (K=896) and down (K=4864) (dense form)"),
-    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true>", 10240, "reference M=39 k_proj (dense form)"),
-    ("gather_decode_kernel<cpq::dev::BF16, 4, 2, true>", 194560, "reference M=39 gate/up (dense form)"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true, true>", 71680, "reference M=39 q, o (K=896) and down (K=4864) (dense form)"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true, true>", 10240, "reference M=39 k_proj (dense form)"),
+    ("gather_decode_kernel<cpq::dev::BF16, 4, 2, true, true>", 194560, "reference M=39 gate/up (dense form)"),
     ("qmm_rows_kernel<cpq::dev::BF16, 4, 3>", 607744, "reference M=39 lm_head (activations in LDS)"),
     ("stream_read_kernel<256, 8, false, false>", 1048576, "cache flush (512 MiB read) before each timed replay"),
     ("stream_read_kernel<256, 8, false, false>", 262144, "read ceiling leg"),

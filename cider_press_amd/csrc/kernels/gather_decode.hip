@@ -85,7 +85,7 @@ __device__ __forceinline__ f32x4 dec_step(const uint32_t* wq, uint32_t sv, uint3
 // DENSE: the same kernel as a small-M matmul (one weight matrix, rows
 // 0..n_rows-1 of x and y; lhs, rhs and status unused): slot u is then the
 // u-th pass of rows_max rows.
-template <typename TT, int BITS, int KW, bool DENSE>
+template <typename TT, int BITS, int KW, bool DENSE, bool WIDE>
 __global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(BITS == 4 ? 4 : 3))) void gather_decode_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     const uint16_t* __restrict__ x, int x_rows, const uint32_t* __restrict__ lhs, const uint32_t* __restrict__ rhs,
@@ -232,19 +232,75 @@ __global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(
         }
       }
       uint32_t wq[PF][BITS];
-      uint32_t sv[PF], bv[PF];
+      // (scale, bias) of each step.  WIDE (group size 64, an even number of
+      // groups per row, so K is a multiple of 128 and every step of the
+      // batch is whole): the column's words for the batch's steps in one or
+      // two wide loads (word T holds step T's two groups; a 2-byte load per
+      // step and value cost the 4-token up projection 3.3 us), then the
+      // lane's halves of steps t, t + 1 packed into one register (the
+      // packed form the vote reads), 16 bits per step.  Otherwise a 16-bit
+      // load per step and value; chunks past K (a partial last step) read
+      // zeros like the slots past the batch.
+      constexpr int NP = WIDE ? (PF + 1) / 2 : PF;
+      uint32_t sv[NP], bv[NP];
       bool live[PF];
 #pragma unroll
       for (int t = 0; t < PF; ++t) {
-        // Chunk (4 step + g) of 32 elements; chunks past K (a partial last
-        // step) read zeros like the slots past the batch.
         const uint32_t ck = (uint32_t)(4 * (js + b0 + t) + g) * 32u;
         live[t] = t < nb && ck < (uint32_t)k;
-        const uint32_t gi = coff0 + (ck >> gs_shift);
-        const uint32_t so = live[t] ? gi * 2u : 0x80000000u;
-        sv[t] = __builtin_amdgcn_raw_buffer_load_b16(sr, so, 0, 0);
-        bv[t] = __builtin_amdgcn_raw_buffer_load_b16(br, so, 0, 0);
       }
+      if constexpr (WIDE) {
+        uint32_t sw[PF], bw[PF];
+        const uint32_t wo = (coff0 + 2u * (uint32_t)(js + b0)) * 2u;  // past 2^31 for columns past N
+        if constexpr (PF >= 4) {
+#pragma unroll
+          for (int q = 0; q < PF; q += 4) {
+            const u32x4 s4 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, wo + 4u * q, 0, 0));
+            const u32x4 b4 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(br, wo + 4u * q, 0, 0));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              sw[q + i] = s4[i];
+              bw[q + i] = b4[i];
+            }
+          }
+        } else if constexpr (PF == 2) {
+          const u32x2 s2 = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(sr, wo, 0, 0));
+          const u32x2 b2 = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(br, wo, 0, 0));
+          sw[0] = s2[0];
+          sw[1] = s2[1];
+          bw[0] = b2[0];
+          bw[1] = b2[1];
+        } else {
+          sw[0] = __builtin_amdgcn_raw_buffer_load_b32(sr, wo, 0, 0);
+          bw[0] = __builtin_amdgcn_raw_buffer_load_b32(br, wo, 0, 0);
+        }
+        // Half g / 2 of words t and t + 1 into bits 0..15 and 16..31.
+        const uint32_t psel = (g >> 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+          const int t1 = 2 * j + 1 < PF ? 2 * j + 1 : 2 * j;
+          sv[j] = __builtin_amdgcn_perm(sw[t1], sw[2 * j], psel);
+          bv[j] = __builtin_amdgcn_perm(bw[t1], bw[2 * j], psel);
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < PF; ++t) {
+          const uint32_t ck = (uint32_t)(4 * (js + b0 + t) + g) * 32u;
+          const uint32_t gi = coff0 + (ck >> gs_shift);
+          const uint32_t so = live[t] ? gi * 2u : 0x80000000u;
+          sv[t] = __builtin_amdgcn_raw_buffer_load_b16(sr, so, 0, 0);
+          bv[t] = __builtin_amdgcn_raw_buffer_load_b16(br, so, 0, 0);
+        }
+      }
+      // Step t's 16-bit scale / bias (bits 0..15 of the result).
+      auto sval = [&](int t) -> uint32_t {
+        if constexpr (WIDE) return (t & 1) ? sv[t >> 1] >> 16 : sv[t >> 1];
+        else return sv[t];
+      };
+      auto bval = [&](int t) -> uint32_t {
+        if constexpr (WIDE) return (t & 1) ? bv[t >> 1] >> 16 : bv[t >> 1];
+        else return bv[t];
+      };
 #pragma unroll
       for (int t = 0; t < PF; ++t)
         dec_load<BITS>(wr, live[t] ? voff0 + (uint32_t)(b0 + t) * (16u * BITS) : 0x80000000u, wq[t]);
@@ -265,15 +321,23 @@ __global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
       for (int t = 0; t < PF; t += 2) {
         const int t1 = t + 1 < PF ? t + 1 : t;
-        const uint32_t sa = live[t] ? sv[t] : kOne, ba = live[t] ? bv[t] : kOne;
-        const uint32_t sb = live[t1] ? sv[t1] : kOne, bb = live[t1] ? bv[t1] : kOne;
-        fast_quick_add<TT>(fq, sa | (sb << 16), ba | (bb << 16));
+        if constexpr (WIDE) {
+          // The packed pair as loaded; slots past the batch count as (1, 1).
+          const uint32_t lo = live[t] ? 0u : 0xffffu, hi = live[t1] ? 0u : 0xffff0000u;
+          const uint32_t one2 = kOne | (kOne << 16);
+          fast_quick_add<TT>(fq, (sv[t >> 1] & ~(lo | hi)) | (one2 & (lo | hi)),
+                             (bv[t >> 1] & ~(lo | hi)) | (one2 & (lo | hi)));
+        } else {
+          const uint32_t sa = live[t] ? sv[t] : kOne, ba = live[t] ? bv[t] : kOne;
+          const uint32_t sb = live[t1] ? sv[t1] : kOne, bb = live[t1] ? bv[t1] : kOne;
+          fast_quick_add<TT>(fq, sa | (sb << 16), ba | (bb << 16));
+        }
       }
       bool fast = ballot(!fast_quick_ok<TT>(fq)) == 0;
       if (!fast) {
         bool ok = true;
 #pragma unroll
-        for (int t = 0; t < PF; ++t) ok &= !live[t] || fast_ok_bits<TT>(sv[t], bv[t]);
+        for (int t = 0; t < PF; ++t) ok &= !live[t] || fast_ok_bits<TT>(sval(t) & 0xffffu, bval(t) & 0xffffu);
         fast = ballot(!ok) == 0;
       }
       // 2d. Multiply: A row m = lane & 15 (rows past the pass read row np-1:
@@ -283,8 +347,8 @@ __global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
       for (int t = 0; t < PF; ++t)
         if (t < nb) {
-          acc = fast ? dec_step<TT, BITS, true>(wq[t], sv[t], bv[t], xrowp + t * 256, m, acc)
-                     : dec_step<TT, BITS, false>(wq[t], sv[t], bv[t], xrowp + t * 256, m, acc);
+          acc = fast ? dec_step<TT, BITS, true>(wq[t], sval(t), bval(t), xrowp + t * 256, m, acc)
+                     : dec_step<TT, BITS, false>(wq[t], sval(t), bval(t), xrowp + t * 256, m, acc);
         }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();  // the next batch restages this wave's region
@@ -320,7 +384,7 @@ __global__ __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(
   }
 }
 
-template <typename TT, int BITS, int KW, bool DENSE>
+template <typename TT, int BITS, int KW, bool DENSE, bool WIDE>
 hipError_t launch_dec(hipStream_t s, const QuantArgs& q, const void* x, int x_rows, const uint32_t* lhs,
                       const uint32_t* rhs, int n_rows, void* y, int n_experts, int n, int k, bool sorted,
                       unsigned int* status) {
@@ -331,7 +395,7 @@ hipError_t launch_dec(hipStream_t s, const QuantArgs& q, const void* x, int x_ro
   const size_t lds = gather_decode_lds(rows_max, k, KW);
   if (lds > 64 * 1024) {
     static const hipError_t attr = [] {
-      const void* fn = reinterpret_cast<const void*>(&gather_decode_kernel<TT, BITS, KW, DENSE>);
+      const void* fn = reinterpret_cast<const void*>(&gather_decode_kernel<TT, BITS, KW, DENSE, WIDE>);
       hipFuncAttributes fa;
       hipError_t e = hipFuncGetAttributes(&fa, fn);
       if (e != hipSuccess) return e;
@@ -343,7 +407,7 @@ hipError_t launch_dec(hipStream_t s, const QuantArgs& q, const void* x, int x_ro
   int gs_shift = 0;
   while ((1 << gs_shift) < q.gs) ++gs_shift;
   const int cols = 16 * (kDecWaves / KW);
-  hipLaunchKernelGGL((gather_decode_kernel<TT, BITS, KW, DENSE>),
+  hipLaunchKernelGGL((gather_decode_kernel<TT, BITS, KW, DENSE, WIDE>),
                      dim3((unsigned)((n + cols - 1) / cols), (unsigned)slots), dim3(64 * kDecWaves), lds, s, q.w,
                      static_cast<const uint16_t*>(q.scales), static_cast<const uint16_t*>(q.biases),
                      static_cast<const uint16_t*>(x), x_rows, lhs, rhs, n_rows, static_cast<uint16_t*>(y), n_experts,
@@ -358,11 +422,19 @@ hipError_t launch_dec_w(hipStream_t s, const QuantArgs& q, const void* x, int x_
   const int slots = DENSE ? (n_rows + kDensePass - 1) / kDensePass : n_rows;
   int kw = gather_decode_kw(slots, n, k, DENSE);
   if (pad_exact && kw == 2) kw = 4;
-  if (kw == 4)
-    return launch_dec<TT, BITS, 4, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
-  if (kw == 2)
-    return launch_dec<TT, BITS, 2, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
-  return launch_dec<TT, BITS, 1, DENSE>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+  // Group size 64 with an even number of groups per row (every column's
+  // row of scales starts on a 32-bit word): the form with wide (scale,
+  // bias) loads.
+  auto go = [&](auto widec) {
+    constexpr bool W = decltype(widec)::value;
+    if (kw == 4)
+      return launch_dec<TT, BITS, 4, DENSE, W>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+    if (kw == 2)
+      return launch_dec<TT, BITS, 2, DENSE, W>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+    return launch_dec<TT, BITS, 1, DENSE, W>(s, q, x, x_rows, lhs, rhs, n_rows, y, n_experts, n, k, sorted, status);
+  };
+  if (q.gs == 64 && ((k / 64) & 1) == 0) return go(std::true_type{});
+  return go(std::false_type{});
 }
 
 template <bool DENSE>
