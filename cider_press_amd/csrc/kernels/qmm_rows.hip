@@ -97,7 +97,7 @@ __device__ __forceinline__ void rows_step(const uint32_t (*wq)[BITS], const uint
   }
 }
 
-template <typename TT, int BITS, int RBK>
+template <typename TT, int BITS, int RBK, bool WIDE>
 __global__ __launch_bounds__(64 * kRowsWaves) __attribute__((amdgpu_waves_per_eu(BITS == 4 && RBK < 4 ? 4 : 3))) void qmm_rows_kernel(
     const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     const uint16_t* __restrict__ x, uint16_t* __restrict__ y, int m, int n, int k, int gs_shift) {
@@ -161,16 +161,70 @@ __global__ __launch_bounds__(64 * kRowsWaves) __attribute__((amdgpu_waves_per_eu
   auto batch = [&](int b0, int nb, auto pfc) {
     constexpr int PF = decltype(pfc)::value;
     uint32_t wq[PF][kRowsNCB][BITS];
-    uint32_t sv[PF][kRowsNCB], bv[PF][kRowsNCB];
+    // (scale, bias) of each step.  WIDE (group size 64, an even number of
+    // groups per row, so every column's row starts on a 32-bit word and K
+    // is a multiple of 128): the column's words for the batch in one or two
+    // 16-byte loads per table (word T holds step T's two groups; a 2-byte
+    // load per step and value is what the routed-decode kernel measured
+    // 3.3 us slower at 4 tokens), the lane's halves of steps t, t + 1 packed
+    // into one register.  Otherwise a 16-bit load per step and value.
+    constexpr int NP = WIDE ? (PF + 1) / 2 : PF;
+    constexpr int NSB = WIDE ? (PF >= 4 ? PF / 4 : 1) : PF;  // loads per table
+    uint32_t sv[NP][kRowsNCB], bv[NP][kRowsNCB];
+    if constexpr (WIDE) {
+      static_assert(kRowsNCB == 1, "one column block per wave");
+      uint32_t sw[PF], bw[PF];
+      const uint32_t wo = (coff0[0] + 2u * (uint32_t)b0) * 2u;  // past 2^31 for columns past N
+      if constexpr (PF >= 4) {
 #pragma unroll
-    for (int t = 0; t < PF; ++t)
+        for (int q = 0; q < PF; q += 4) {
+          const u32x4 s4 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, wo + 4u * q, 0, 0));
+          const u32x4 b4 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(br, wo + 4u * q, 0, 0));
 #pragma unroll
-      for (int c = 0; c < kRowsNCB; ++c) {
-        const uint32_t gi = coff0[c] + (((uint32_t)(4 * (b0 + t) + g) * 32u) >> gs_shift);
-        const uint32_t so = t < nb ? gi * 2u : 0x80000000u;
-        sv[t][c] = __builtin_amdgcn_raw_buffer_load_b16(sr, so, 0, 0);
-        bv[t][c] = __builtin_amdgcn_raw_buffer_load_b16(br, so, 0, 0);
+          for (int i = 0; i < 4; ++i) {
+            sw[q + i] = s4[i];
+            bw[q + i] = b4[i];
+          }
+        }
+      } else if constexpr (PF == 2) {
+        const u32x2 s2 = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(sr, wo, 0, 0));
+        const u32x2 b2 = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(br, wo, 0, 0));
+        sw[0] = s2[0];
+        sw[1] = s2[1];
+        bw[0] = b2[0];
+        bw[1] = b2[1];
+      } else {
+        sw[0] = __builtin_amdgcn_raw_buffer_load_b32(sr, wo, 0, 0);
+        bw[0] = __builtin_amdgcn_raw_buffer_load_b32(br, wo, 0, 0);
       }
+      // Half g / 2 of words t and t + 1 into bits 0..15 and 16..31.
+      const uint32_t psel = (g >> 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+      for (int j = 0; j < NP; ++j) {
+        const int t1 = 2 * j + 1 < PF ? 2 * j + 1 : 2 * j;
+        sv[j][0] = __builtin_amdgcn_perm(sw[t1], sw[2 * j], psel);
+        bv[j][0] = __builtin_amdgcn_perm(bw[t1], bw[2 * j], psel);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < PF; ++t)
+#pragma unroll
+        for (int c = 0; c < kRowsNCB; ++c) {
+          const uint32_t gi = coff0[c] + (((uint32_t)(4 * (b0 + t) + g) * 32u) >> gs_shift);
+          const uint32_t so = t < nb ? gi * 2u : 0x80000000u;
+          sv[t][c] = __builtin_amdgcn_raw_buffer_load_b16(sr, so, 0, 0);
+          bv[t][c] = __builtin_amdgcn_raw_buffer_load_b16(br, so, 0, 0);
+        }
+    }
+    // Step t's 16-bit scale / bias of column block c (bits 0..15).
+    auto sval = [&](int t, int c) -> uint32_t {
+      if constexpr (WIDE) return (t & 1) ? sv[t >> 1][c] >> 16 : sv[t >> 1][c] & 0xffffu;
+      else return sv[t][c];
+    };
+    auto bval = [&](int t, int c) -> uint32_t {
+      if constexpr (WIDE) return (t & 1) ? bv[t >> 1][c] >> 16 : bv[t >> 1][c] & 0xffffu;
+      else return bv[t][c];
+    };
 #pragma unroll
     for (int t = 0; t < PF; ++t)
 #pragma unroll
@@ -178,7 +232,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) __attribute__((amdgpu_waves_per_eu
         rows_load<BITS>(wr, t < nb ? voff0[c] + (uint32_t)(b0 + t) * (16u * BITS) : 0x80000000u, wq[t][c]);
     if (b0 == 0) {
       // The activation copies are older than this batch's loads.
-      wait_vmcnt<PF * kRowsNCB * (2 + BITS / 4)>();
+      wait_vmcnt<kRowsNCB * (2 * NSB + PF * (BITS / 4))>();
       __syncthreads();
     }
     // Vote: the packed exponent check over the batch's (scale, bias) pairs
@@ -191,8 +245,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
       for (int t = 0; t < PF; t += 2) {
         const int t1 = t + 1 < PF ? t + 1 : t;
-        const uint32_t s0 = t < nb ? sv[t][c] : sv[0][c], b0v = t < nb ? bv[t][c] : bv[0][c];
-        const uint32_t s1 = t1 < nb ? sv[t1][c] : sv[0][c], b1v = t1 < nb ? bv[t1][c] : bv[0][c];
+        const uint32_t s0 = t < nb ? sval(t, c) : sval(0, c), b0v = t < nb ? bval(t, c) : bval(0, c);
+        const uint32_t s1 = t1 < nb ? sval(t1, c) : sval(0, c), b1v = t1 < nb ? bval(t1, c) : bval(0, c);
         fast_quick_add<TT>(fq, s0 | (s1 << 16), b0v | (b1v << 16));
       }
     bool fast = rows_ballot(!fast_quick_ok<TT>(fq)) == 0;
@@ -201,17 +255,23 @@ __global__ __launch_bounds__(64 * kRowsWaves) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
       for (int t = 0; t < PF; ++t)
 #pragma unroll
-        for (int c = 0; c < kRowsNCB; ++c) ok &= t >= nb || fast_ok_bits<TT>(sv[t][c], bv[t][c]);
+        for (int c = 0; c < kRowsNCB; ++c) ok &= t >= nb || fast_ok_bits<TT>(sval(t, c), bval(t, c));
       fast = rows_ballot(!ok) == 0;
     }
 #pragma unroll
     for (int t = 0; t < PF; ++t)
       if (t < nb) {
         const unsigned char* xs = smem + (b0 + t) * 256;
+        uint32_t st[kRowsNCB], bt[kRowsNCB];
+#pragma unroll
+        for (int c = 0; c < kRowsNCB; ++c) {
+          st[c] = sval(t, c);
+          bt[c] = bval(t, c);
+        }
         if (fast)
-          rows_step<TT, BITS, true, RBK>(wq[t], sv[t], bv[t], xs, rstride, rows, acc);
+          rows_step<TT, BITS, true, RBK>(wq[t], st, bt, xs, rstride, rows, acc);
         else
-          rows_step<TT, BITS, false, RBK>(wq[t], sv[t], bv[t], xs, rstride, rows, acc);
+          rows_step<TT, BITS, false, RBK>(wq[t], st, bt, xs, rstride, rows, acc);
       }
   };
   for (int b0 = 0; b0 < S; b0 += PFMAX) {
@@ -250,12 +310,12 @@ __global__ __launch_bounds__(64 * kRowsWaves) __attribute__((amdgpu_waves_per_eu
 
 size_t rows_lds(int m, int k) { return (size_t)m * (size_t)((k / 128 + 3) / 4) * 1024; }
 
-template <typename TT, int BITS, int RBK>
+template <typename TT, int BITS, int RBK, bool WIDE>
 hipError_t launch_rows_t(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k) {
   const size_t lds = rows_lds(m, k);
   if (lds > 64 * 1024) {
     static const hipError_t attr = [] {
-      const void* fn = reinterpret_cast<const void*>(&qmm_rows_kernel<TT, BITS, RBK>);
+      const void* fn = reinterpret_cast<const void*>(&qmm_rows_kernel<TT, BITS, RBK, WIDE>);
       hipFuncAttributes fa;
       hipError_t e = hipFuncGetAttributes(&fa, fn);
       if (e != hipSuccess) return e;
@@ -266,19 +326,27 @@ hipError_t launch_rows_t(hipStream_t s, const QuantArgs& q, const void* x, void*
   }
   int gs_shift = 0;
   while ((1 << gs_shift) < q.gs) ++gs_shift;
-  hipLaunchKernelGGL((qmm_rows_kernel<TT, BITS, RBK>), dim3((unsigned)((n + kRowsCols - 1) / kRowsCols)),
+  hipLaunchKernelGGL((qmm_rows_kernel<TT, BITS, RBK, WIDE>), dim3((unsigned)((n + kRowsCols - 1) / kRowsCols)),
                      dim3(64 * kRowsWaves), lds, s, q.w, static_cast<const uint16_t*>(q.scales),
                      static_cast<const uint16_t*>(q.biases), static_cast<const uint16_t*>(x),
                      static_cast<uint16_t*>(y), m, n, k, gs_shift);
   return hipGetLastError();
 }
 
+template <typename TT, int BITS, bool WIDE>
+hipError_t launch_rows_w(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k) {
+  if (m <= 16) return launch_rows_t<TT, BITS, 1, WIDE>(s, q, x, y, m, n, k);
+  if (m <= 32) return launch_rows_t<TT, BITS, 2, WIDE>(s, q, x, y, m, n, k);
+  if (m <= 48) return launch_rows_t<TT, BITS, 3, WIDE>(s, q, x, y, m, n, k);
+  return launch_rows_t<TT, BITS, 4, WIDE>(s, q, x, y, m, n, k);
+}
+
+// Group size 64 with an even number of groups per row: the form with wide
+// (scale, bias) loads.
 template <typename TT, int BITS>
 hipError_t launch_rows_b(hipStream_t s, const QuantArgs& q, const void* x, void* y, int m, int n, int k) {
-  if (m <= 16) return launch_rows_t<TT, BITS, 1>(s, q, x, y, m, n, k);
-  if (m <= 32) return launch_rows_t<TT, BITS, 2>(s, q, x, y, m, n, k);
-  if (m <= 48) return launch_rows_t<TT, BITS, 3>(s, q, x, y, m, n, k);
-  return launch_rows_t<TT, BITS, 4>(s, q, x, y, m, n, k);
+  if (q.gs == 64 && ((k / 64) & 1) == 0) return launch_rows_w<TT, BITS, true>(s, q, x, y, m, n, k);
+  return launch_rows_w<TT, BITS, false>(s, q, x, y, m, n, k);
 }
 
 }  // namespace
