@@ -840,7 +840,7 @@ TRACE_WORKLOADS = (
     ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true, true>", 71680, "reference M=39 q, o (K=896) and down (K=4864) (dense form)"),
     ("gather_decode_kernel<cpq::dev::BF16, 4, 4, true, true>", 10240, "reference M=39 k_proj (dense form)"),
     ("gather_decode_kernel<cpq::dev::BF16, 4, 2, true, true>", 194560, "reference M=39 gate/up (dense form)"),
-    ("qmm_rows_kernel<cpq::dev::BF16, 4, 3>", 607744, "reference M=39 lm_head (activations in LDS)"),
+    ("qmm_rows_kernel<cpq::dev::BF16, 4, 3, true>", 607744, "reference M=39 lm_head (activations in LDS)"),
     ("stream_read_kernel<256, 8, false, false>", 1048576, "cache flush (512 MiB read) before each timed replay"),
     ("stream_read_kernel<256, 8, false, false>", 262144, "read ceiling leg"),
     ("stream_read_kernel<256, 4, false, false>", 256, "launch floor (one workgroup, 16 B)"),
