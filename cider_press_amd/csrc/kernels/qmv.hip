@@ -106,17 +106,30 @@ __device__ __forceinline__ f32x4 group_consts(uint32_t sv, uint32_t bv) {
 }
 
 // One chunk (BITS words) of a weight row through a buffer descriptor.
-template <int BITS>
-__device__ __forceinline__ void lean_load(__amdgpu_buffer_rsrc_t wr, uint32_t voff, int soff, uint32_t* dst) {
+// One chunk of a lane's weight stream (16 bytes at 4 bits, 32 at 8).  NT
+// sets the non-temporal policy (streamed once; the weights need not stay in
+// the caches).  Measured on the 4-bit decode layout with M rows: M = 4 /
+// 16 at N = K = 4096 4.85 -> 4.46 / 6.11 -> 5.95 us on two boxes.  The
+// M = 1 decode kernel at cfg2a moved by -0.17 us on one box and +0.19 us on
+// another, and cfg2b, cfg1 and the 8-bit step-interleaved rows were slower
+// with it, so they keep the default policy.
+template <int BITS, bool NT>
+__device__ __forceinline__ void lean_load_nt(__amdgpu_buffer_rsrc_t wr, uint32_t voff, int soff, uint32_t* dst) {
+  constexpr int POL = NT ? 2 : 0;  // cache policy: nt
   if constexpr (BITS == 4) {
-    const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff, soff, 0));
+    const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff, soff, POL));
     dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
   } else {
-    const u32x4 v0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff, soff, 0));
-    const u32x4 v1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff + 16, soff, 0));
+    const u32x4 v0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff, soff, POL));
+    const u32x4 v1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff + 16, soff, POL));
     dst[0] = v0.x; dst[1] = v0.y; dst[2] = v0.z; dst[3] = v0.w;
     dst[4] = v1.x; dst[5] = v1.y; dst[6] = v1.z; dst[7] = v1.w;
   }
+}
+
+template <int BITS>
+__device__ __forceinline__ void lean_load(__amdgpu_buffer_rsrc_t wr, uint32_t voff, int soff, uint32_t* dst) {
+  lean_load_nt<BITS, false>(wr, voff, soff, dst);
 }
 
 template <typename TT, int BITS, int WAVES, int PF, bool EXACT>
@@ -639,7 +652,7 @@ __global__ __launch_bounds__(64 * WAVES) void qmm_lean_rows_kernel(const uint32_
                                               xr, xoff + 1024u * t, (int)((uint32_t)rr * (uint32_t)k * 2u), 0));
     }
 #pragma unroll
-    for (int p = 0; p < PF; ++p) lean_load<BITS>(wr, voff + p * 4 * CB, 0, buf[p]);
+    for (int p = 0; p < PF; ++p) lean_load_nt<BITS, BITS == 4>(wr, voff + p * 4 * CB, 0, buf[p]);
 #pragma unroll
     for (int i = 0; i < XMAX; ++i) {
       const int rr = i / IPR, t = i % IPR;
